@@ -1,0 +1,145 @@
+// extern "C" entry points of libspmm_mi355x: argument validation, workspace
+// sizing and dispatch to the kernels.  The checks mirror the reference's
+// operator contracts (extension/custom_op.cpp:36-152) at the level of sizes
+// and dtypes; tensor-level checks (device, rank, contiguity) live in the torch
+// extension that calls this library.
+#include <string>
+
+#include "common.h"
+
+namespace spmm {
+
+namespace {
+thread_local std::string g_last_error;
+}
+
+void set_error(const std::string& msg) { g_last_error = msg; }
+void clear_error() { g_last_error.clear(); }
+
+spmm_status fail(spmm_status code, const std::string& msg) {
+  set_error(msg);
+  return code;
+}
+
+spmm_status check_hip(hipError_t err, const char* what) {
+  if (err == hipSuccess) return SPMM_OK;
+  return fail(SPMM_ERR_DEVICE, std::string(what) + ": " + hipGetErrorString(err));
+}
+
+spmm_status check_launch(const char* what) { return check_hip(hipGetLastError(), what); }
+
+namespace {
+
+spmm_status check_types(int32_t index_type, int32_t value_type, const char* op) {
+  if (index_type != SPMM_INDEX_I32 && index_type != SPMM_INDEX_I64)
+    return fail(SPMM_ERR_CONTRACT, std::string(op) + ": index arrays must be int32 or int64");
+  if (value_type != SPMM_VALUE_F16 && value_type != SPMM_VALUE_F32)
+    return fail(SPMM_ERR_CONTRACT, std::string(op) + " supports only FP16 and FP32 dense tensors");
+  return SPMM_OK;
+}
+
+// Feature-width contract of check_dense_contract (extension/custom_op.cpp:39-57).
+spmm_status check_width(int64_t width, int32_t value_type, int64_t alignment, const char* op) {
+  const bool half = value_type == SPMM_VALUE_F16;
+  const int64_t max_width = half ? 1024 : 512;
+  if (width <= 0 || width > max_width)
+    return fail(SPMM_ERR_CONTRACT, std::string(op) + " requires 0 < feature width <= " +
+                                       std::to_string(max_width) + " for " +
+                                       (half ? "FP16" : "FP32") + ", but got " +
+                                       std::to_string(width));
+  if (width % alignment != 0)
+    return fail(SPMM_ERR_CONTRACT,
+                std::string(op) + " requires feature width divisible by " +
+                    std::to_string(alignment) + ", but got " + std::to_string(width) +
+                    ". Pad and crop the dense tensor or use a safe PyTorch fallback.");
+  return SPMM_OK;
+}
+
+}  // namespace
+}  // namespace spmm
+
+using namespace spmm;
+
+extern "C" {
+
+const char* spmm_last_error(void) { return g_last_error.c_str(); }
+
+const char* spmm_version(void) { return "spmm_mi355x 0.1 gfx950"; }
+
+spmm_status spmm_csr_workspace(const spmm_csr_desc* d, size_t* bytes) {
+  clear_error();
+  if (d == nullptr || bytes == nullptr) return fail(SPMM_ERR_INVALID_ARGUMENT, "null argument");
+  if (spmm_status st = check_types(d->index_type, d->value_type, "spmm_csr")) return st;
+  *bytes = gather_workspace_bytes(d->nnz < 0 ? 0 : d->nnz, d->width);
+  return SPMM_OK;
+}
+
+spmm_status spmm_csr_run(const spmm_csr_desc* d, const void* rowptr, const void* col,
+                         const void* value, const void* dense, void* out, void* workspace,
+                         size_t workspace_bytes, spmm_stream stream) {
+  clear_error();
+  if (d == nullptr) return fail(SPMM_ERR_INVALID_ARGUMENT, "null descriptor");
+  if (spmm_status st = check_types(d->index_type, d->value_type, "spmm_csr")) return st;
+  if (spmm_status st = check_width(d->width, d->value_type,
+                                   d->value_type == SPMM_VALUE_F16 ? 16 : 8, "spmm_csr"))
+    return st;
+  if (d->rows < 0 || d->nnz < 0 || d->dense_rows < 0)
+    return fail(SPMM_ERR_CONTRACT, "spmm_csr: negative extent");
+  if (d->rows == 0) return SPMM_OK;
+  if (rowptr == nullptr || out == nullptr || (d->nnz > 0 && (col == nullptr || value == nullptr)) ||
+      (d->dense_rows > 0 && dense == nullptr))
+    return fail(SPMM_ERR_INVALID_ARGUMENT, "spmm_csr: null device pointer");
+  return launch_gather(d->index_type, d->value_type, rowptr, col, value, d->nnz, 0, d->rows,
+                       dense, d->dense_rows, d->width, out, workspace, workspace_bytes,
+                       as_stream(stream));
+}
+
+int64_t spmm_mixed_out_rows(const spmm_mixed_desc* d) {
+  if (d == nullptr) return -1;
+  const int64_t blocks = 16 * (d->block_windows < 0 ? 0 : d->block_windows);
+  const int64_t vec = d->vector_rows < 0 ? 0 : d->vector_rows;
+  return blocks > vec ? blocks : vec;
+}
+
+spmm_status spmm_mixed_workspace(const spmm_mixed_desc* d, size_t* bytes) {
+  clear_error();
+  if (d == nullptr || bytes == nullptr) return fail(SPMM_ERR_INVALID_ARGUMENT, "null argument");
+  if (spmm_status st = check_types(d->index_type, d->value_type, "spmm_ascend_cube")) return st;
+  *bytes = gather_workspace_bytes(d->vector_nnz < 0 ? 0 : d->vector_nnz, d->width);
+  return SPMM_OK;
+}
+
+spmm_status spmm_mixed_run(const spmm_mixed_desc* d, const void* Crowptr, const void* Ccol,
+                           const void* Cvalue, const void* Vrowptr, const void* Vcol,
+                           const void* Vvalue, const void* dense, void* out, void* workspace,
+                           size_t workspace_bytes, spmm_stream stream) {
+  clear_error();
+  if (d == nullptr) return fail(SPMM_ERR_INVALID_ARGUMENT, "null descriptor");
+  if (spmm_status st = check_types(d->index_type, d->value_type, "spmm_ascend_cube")) return st;
+  if (spmm_status st = check_width(d->width, d->value_type, 16, "spmm_ascend_cube")) return st;
+  if (d->block_windows < 0 || d->block_count < 0 || d->block_values < 0 || d->vector_rows < 0 ||
+      d->vector_nnz < 0 || d->dense_rows < 0)
+    return fail(SPMM_ERR_CONTRACT, "spmm_ascend_cube: negative extent");
+  const int64_t out_rows = spmm_mixed_out_rows(d);
+  if (out_rows == 0) return SPMM_OK;
+  if (out == nullptr || (d->dense_rows > 0 && dense == nullptr) ||
+      (d->block_windows > 0 && Crowptr == nullptr) ||
+      (d->block_count > 0 && (Ccol == nullptr || Cvalue == nullptr)) ||
+      (d->vector_rows > 0 && Vrowptr == nullptr) ||
+      (d->vector_nnz > 0 && (Vcol == nullptr || Vvalue == nullptr)))
+    return fail(SPMM_ERR_INVALID_ARGUMENT, "spmm_ascend_cube: null device pointer");
+  hipStream_t s = as_stream(stream);
+  const int64_t block_rows = 16 * d->block_windows;
+  spmm_status st =
+      launch_block(d->index_type, d->value_type, Crowptr, Ccol, Cvalue, d->block_windows,
+                   d->block_count, d->block_values, Vrowptr, Vcol, Vvalue, d->vector_rows,
+                   d->vector_nnz, dense, d->dense_rows, d->width, out, s);
+  if (st != SPMM_OK) return st;
+  if (d->vector_rows > block_rows)
+    st = launch_gather(d->index_type, d->value_type, Vrowptr, Vcol, Vvalue, d->vector_nnz,
+                       block_rows, d->vector_rows, dense, d->dense_rows, d->width, out,
+                       workspace, workspace_bytes, s);
+  return st;
+}
+
+}  // extern "C"

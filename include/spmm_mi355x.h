@@ -1,0 +1,168 @@
+/*
+ * spmm_mi355x.h — C ABI of the MI355X (gfx950) SpMM library `libspmm_mi355x.so`.
+ *
+ * This is the drop-in boundary for the SpMM hot path of Ascend-SpMM.  Every
+ * entry point below replaces one call site of the reference's CANN/aclnn
+ * layer or one of its host-side preprocessing routines; the citation next to
+ * each declaration names the reference code it stands in for (paths are
+ * relative to the Ascend-SpMM repository root).
+ *
+ * Conventions
+ *  - Plain pointers and sizes only; no C++ or torch types cross this boundary.
+ *  - All device pointers are HIP device memory owned by the caller.  The
+ *    library never allocates device memory for its outputs; scratch space is
+ *    the caller-provided workspace, sized by the matching *_workspace call.
+ *  - Launches are asynchronous on the given stream unless the comment says
+ *    the call synchronises (the *_plan calls read a few sizes back).
+ *  - Index arrays of one call share one index type (int32 or int64); value
+ *    arrays and the dense operand share one value type (fp16 or fp32).
+ *  - Kernels never read outside the extents passed in: row pointers are
+ *    clamped to the index arrays and out-of-range column ids contribute zero.
+ *  - On failure a call returns a non-zero spmm_status and records a message
+ *    retrievable (per thread) with spmm_last_error().
+ *  - Reentrant: calls on different streams may run concurrently.
+ */
+#ifndef SPMM_MI355X_H_
+#define SPMM_MI355X_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes.  Each maps to one Python exception type in the extension,
+ * matching what the reference raises for the same condition:
+ * INVALID_ARGUMENT -> ValueError   (std::invalid_argument in the reference)
+ * OUT_OF_RANGE     -> IndexError   (std::out_of_range)
+ * OVERFLOW         -> OverflowError(std::overflow_error)
+ * CONTRACT         -> RuntimeError (TORCH_CHECK failures)
+ * DEVICE           -> RuntimeError (a HIP runtime error) */
+typedef enum spmm_status {
+  SPMM_OK = 0,
+  SPMM_ERR_INVALID_ARGUMENT = 1,
+  SPMM_ERR_OUT_OF_RANGE = 2,
+  SPMM_ERR_OVERFLOW = 3,
+  SPMM_ERR_CONTRACT = 4,
+  SPMM_ERR_DEVICE = 5
+} spmm_status;
+
+typedef enum spmm_index_type { SPMM_INDEX_I32 = 0, SPMM_INDEX_I64 = 1 } spmm_index_type;
+typedef enum spmm_value_type { SPMM_VALUE_F16 = 0, SPMM_VALUE_F32 = 1, SPMM_VALUE_F64 = 2 } spmm_value_type;
+
+/* Opaque HIP stream (hipStream_t); NULL is the default stream. */
+typedef void* spmm_stream;
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* spmm_last_error(void);
+
+/* Library version string, e.g. "spmm_mi355x 0.1 gfx950". */
+const char* spmm_version(void);
+
+/* ------------------------------------------------------------------------
+ * spmm_csr — C[M,N] = A[M,K] (CSR) x dense[K,N]
+ *
+ * Replaces EXEC_NPU_CMD(aclnnSpmmCsr, ...) in spmm_csr_impl_npu
+ * (extension/custom_op.cpp:67-88) and the tiling + kernel behind it
+ * (kernels/op_host/spmm_csr.cpp:8-35, kernels/op_kernel/spmm_csr.cpp:226-569).
+ * The reference's per-core `start` array is a tiling aid; the MI355X kernel
+ * partitions on the device, so `start` is not an argument here.
+ *
+ * Every output row is written (rows without nonzeros become zero), so `out`
+ * need not be cleared.  Each row is accumulated in fp32 in nonzero order and
+ * rounded once to the value type (round-to-nearest-even).  Rows longer than
+ * the library's fixed split length are cut at split points that depend only
+ * on the row pointer, and their fp32 pieces are added in order, so results are
+ * deterministic and identical for every feature width N.
+ * ---------------------------------------------------------------------- */
+typedef struct spmm_csr_desc {
+  int64_t rows;        /* M: rowptr holds rows + 1 entries                 */
+  int64_t nnz;         /* extent of col[] and value[]                      */
+  int64_t dense_rows;  /* K: rows of dense                                 */
+  int64_t width;       /* N: columns of dense and out (row-major, contiguous) */
+  int32_t index_type;  /* spmm_index_type                                  */
+  int32_t value_type;  /* spmm_value_type (F16 or F32)                     */
+} spmm_csr_desc;
+
+spmm_status spmm_csr_workspace(const spmm_csr_desc* desc, size_t* bytes);
+
+spmm_status spmm_csr_run(const spmm_csr_desc* desc,
+                         const void* rowptr, const void* col, const void* value,
+                         const void* dense, void* out,
+                         void* workspace, size_t workspace_bytes,
+                         spmm_stream stream);
+
+/* ------------------------------------------------------------------------
+ * spmm_mixed — the spmm_ascend_cube operator:
+ *   out[16*s + r, :]  = sum_{b in [Crowptr[s], Crowptr[s+1])} Cvalue[16*b + r] * dense[Ccol[b], :]
+ *   out[i, :]        += sum_{p in [Vrowptr[i], Vrowptr[i+1])} Vvalue[p] * dense[Vcol[p], :]
+ * with out rows = max(16 * block_windows, vector_rows).
+ *
+ * Replaces EXEC_NPU_CMD(aclnnSpmmAscendCube, ...) in spmm_ascend_cube_impl_npu
+ * (extension/custom_op.cpp:115-152), its tiling
+ * (kernels/op_host/spmm_ascend_cube.cpp:8-51) and the mixed AIC/AIV kernel
+ * (kernels/op_kernel/spmm_ascend_cube.cpp:16-311, 543-907).  The per-core
+ * Cstart/Vstart arrays of the reference are not needed.
+ *
+ * The block part (16x1 BCSR windows) runs on fp16/fp32 MFMA; rows of block
+ * windows also take their vector-part nonzeros in the same work-group, added
+ * after the block sum.  Rows at or beyond 16*block_windows take the CSR gather
+ * path of spmm_csr, so with block_windows == 0 the result is bit-identical to
+ * spmm_csr on the same CSR.  Every output row is written.
+ * ---------------------------------------------------------------------- */
+typedef struct spmm_mixed_desc {
+  int64_t block_windows;  /* Crowptr.numel - 1                              */
+  int64_t block_count;    /* Ccol_ids.numel                                 */
+  int64_t block_values;   /* Cvalue.numel (>= 16 * blocks referenced)       */
+  int64_t vector_rows;    /* Vrowptr.numel - 1                              */
+  int64_t vector_nnz;     /* min(Vcol_ids.numel, Vvalue.numel)              */
+  int64_t dense_rows;     /* K                                              */
+  int64_t width;          /* N                                              */
+  int32_t index_type;
+  int32_t value_type;
+} spmm_mixed_desc;
+
+spmm_status spmm_mixed_workspace(const spmm_mixed_desc* desc, size_t* bytes);
+
+spmm_status spmm_mixed_run(const spmm_mixed_desc* desc,
+                           const void* Crowptr, const void* Ccol, const void* Cvalue,
+                           const void* Vrowptr, const void* Vcol, const void* Vvalue,
+                           const void* dense, void* out,
+                           void* workspace, size_t workspace_bytes,
+                           spmm_stream stream);
+
+/* Number of output rows spmm_mixed_run writes: max(16*block_windows, vector_rows). */
+int64_t spmm_mixed_out_rows(const spmm_mixed_desc* desc);
+
+/* ------------------------------------------------------------------------
+ * Row permutation of a node tensor (P and P^T of the graph layout).
+ *
+ * spmm_pack_rows:    packed[inv[i], :] = src[i, :] for i < rows; every other
+ *                    packed row is zero (if inv repeats a packed row, the
+ *                    largest i wins).  Replaces pack_node_tensor's
+ *                    new_zeros + index_copy_ (spmm_npu.py:23-47).  Needs a
+ *                    workspace of spmm_pack_workspace(packed_rows) bytes.
+ * spmm_restore_rows: dst[i, :] = packed[inv[i], :].  Replaces
+ *                    restore_node_tensor's index_select (spmm_npu.py:50-62).
+ * `row_bytes` is the byte size of one row (any element type).  `inv` is int64.
+ * Entries of inv outside [0, packed_rows) are skipped by pack and give a zero
+ * row in restore (the Python layer rejects them before the call, as the
+ * reference does).
+ * ---------------------------------------------------------------------- */
+size_t spmm_pack_workspace(int64_t packed_rows);
+
+spmm_status spmm_pack_rows(const void* src, int64_t rows, int64_t row_bytes,
+                           const int64_t* inv, void* packed, int64_t packed_rows,
+                           void* workspace, size_t workspace_bytes,
+                           spmm_stream stream);
+
+spmm_status spmm_restore_rows(const void* packed, int64_t packed_rows, int64_t row_bytes,
+                              const int64_t* inv, int64_t rows, void* dst,
+                              spmm_stream stream);
+
+#ifdef __cplusplus
+}  /* extern "C" */
+#endif
+
+#endif  /* SPMM_MI355X_H_ */

@@ -1,0 +1,127 @@
+"""The C ABI of libspmm_mi355x.so: every function declared in include/*.h is
+exported (CPU), host-side validation answers without a GPU (CPU), and direct
+ctypes calls of the run entry points match the oracle (GPU)."""
+
+import ctypes
+import glob
+import os
+import re
+
+import numpy as np
+import pytest
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB = os.path.join(REPO, "ascend-spmm_amd", "libspmm_mi355x.so")
+
+
+def declared_functions():
+    names = []
+    for header in glob.glob(os.path.join(REPO, "include", "*.h")):
+        text = open(header).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names += re.findall(r"^\s*[A-Za-z_][\w\s\*]*?\b(spmm_\w+)\s*\(", text, flags=re.M)
+    return sorted(set(names))
+
+
+class CsrDesc(ctypes.Structure):
+    _fields_ = [("rows", ctypes.c_int64), ("nnz", ctypes.c_int64), ("dense_rows", ctypes.c_int64),
+                ("width", ctypes.c_int64), ("index_type", ctypes.c_int32),
+                ("value_type", ctypes.c_int32)]
+
+
+class MixedDesc(ctypes.Structure):
+    _fields_ = [("block_windows", ctypes.c_int64), ("block_count", ctypes.c_int64),
+                ("block_values", ctypes.c_int64), ("vector_rows", ctypes.c_int64),
+                ("vector_nnz", ctypes.c_int64), ("dense_rows", ctypes.c_int64),
+                ("width", ctypes.c_int64), ("index_type", ctypes.c_int32),
+                ("value_type", ctypes.c_int32)]
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(LIB):
+        pytest.fail(f"{LIB} is not built (python ascend-spmm_amd/build.py)")
+    lib = ctypes.CDLL(LIB)
+    lib.spmm_last_error.restype = ctypes.c_char_p
+    lib.spmm_version.restype = ctypes.c_char_p
+    lib.spmm_mixed_out_rows.restype = ctypes.c_int64
+    lib.spmm_pack_workspace.restype = ctypes.c_size_t
+    return lib
+
+
+def test_header_declares_entry_points():
+    names = declared_functions()
+    for required in ("spmm_csr_run", "spmm_csr_workspace", "spmm_mixed_run",
+                     "spmm_mixed_workspace", "spmm_pack_rows", "spmm_restore_rows",
+                     "spmm_last_error"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, f"not exported: {missing}"
+    assert lib.spmm_version().startswith(b"spmm_mi355x")
+
+
+def test_host_validation_without_gpu(lib):
+    d = CsrDesc(10, 5, 10, 24, 0, 0)  # fp16 width 24: not divisible by 16
+    rc = lib.spmm_csr_run(ctypes.byref(d), None, None, None, None, None, None, 0, None)
+    assert rc == 4 and b"divisible by 16" in lib.spmm_last_error()
+    d = CsrDesc(10, 5, 10, 1040, 0, 0)
+    assert lib.spmm_csr_run(ctypes.byref(d), None, None, None, None, None, None, 0, None) == 4
+    assert b"<= 1024 for FP16" in lib.spmm_last_error()
+    d = CsrDesc(10, 5, 10, 16, 7, 0)  # bad index type
+    assert lib.spmm_csr_run(ctypes.byref(d), None, None, None, None, None, None, 0, None) == 4
+    d = CsrDesc(10, 5, 10, 16, 0, 0)
+    assert lib.spmm_csr_run(ctypes.byref(d), None, None, None, None, None, None, 0, None) == 1
+    size = ctypes.c_size_t(0)
+    assert lib.spmm_csr_workspace(ctypes.byref(d), ctypes.byref(size)) == 0
+    m = MixedDesc(3, 0, 0, 100, 0, 10, 16, 0, 0)
+    assert lib.spmm_mixed_out_rows(ctypes.byref(m)) == 100
+    m.block_windows = 10
+    assert lib.spmm_mixed_out_rows(ctypes.byref(m)) == 160
+    assert lib.spmm_pack_workspace(ctypes.c_int64(100)) == 800
+
+
+@pytest.mark.gpu
+def test_direct_cabi_calls_match_oracle(lib):
+    import torch
+
+    import oracle as O
+
+    rng = np.random.default_rng(5)
+    rows, K, N = 200, 150, 64
+    deg = rng.integers(0, 30, rows)
+    crow = np.zeros(rows + 1, np.int64)
+    crow[1:] = np.cumsum(deg)
+    col = np.concatenate([np.sort(rng.choice(K, d, replace=False)) for d in deg]).astype(np.int64)
+    vals = rng.uniform(-1, 1, col.size).astype(np.float32)
+    B = rng.standard_normal((K, N)).astype(np.float32)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    d_crow, d_col = t(crow.astype(np.int32)), t(col.astype(np.int32))
+    d_val, d_B = t(vals), t(B)
+    out = torch.empty(rows, N, device="cuda")
+    d = CsrDesc(rows, col.size, K, N, 0, 1)
+    ws_bytes = ctypes.c_size_t(0)
+    assert lib.spmm_csr_workspace(ctypes.byref(d), ctypes.byref(ws_bytes)) == 0
+    ws = torch.empty(max(ws_bytes.value, 1), dtype=torch.uint8, device="cuda")
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    p = lambda x: ctypes.c_void_p(x.data_ptr())
+    rc = lib.spmm_csr_run(ctypes.byref(d), p(d_crow), p(d_col), p(d_val), p(d_B), p(out), p(ws),
+                          ctypes.c_size_t(ws_bytes.value), stream)
+    assert rc == 0, lib.spmm_last_error()
+    torch.cuda.synchronize()
+    expected = O.spmm_f64(crow, col, vals, B)
+    assert np.allclose(out.cpu().numpy(), expected, atol=1e-4, rtol=1e-4)
+
+    # the mixed entry point with an empty block part is bitwise spmm_csr
+    out2 = torch.empty(rows, N, device="cuda")
+    zero = torch.zeros(1, dtype=torch.int32, device="cuda")
+    m = MixedDesc(0, 0, 0, rows, col.size, K, N, 0, 1)
+    assert lib.spmm_mixed_workspace(ctypes.byref(m), ctypes.byref(ws_bytes)) == 0
+    ws2 = torch.empty(max(ws_bytes.value, 1), dtype=torch.uint8, device="cuda")
+    rc = lib.spmm_mixed_run(ctypes.byref(m), p(zero), None, None, p(d_crow), p(d_col), p(d_val),
+                            p(d_B), p(out2), p(ws2), ctypes.c_size_t(ws_bytes.value), stream)
+    assert rc == 0, lib.spmm_last_error()
+    torch.cuda.synchronize()
+    assert torch.equal(out.cpu(), out2.cpu())

@@ -1,0 +1,300 @@
+"""GPU parity tests of the SpMM operators (spmm_csr, spmm_ascend_cube and the
+ablation aliases) against the CPU oracle.
+
+Tolerances are the reference's (tests/task_mapping/correctness.py:140-143):
+atol = rtol = 2e-2 for fp16 and 1e-4 for fp32, applied to the fp64 oracle.
+The vector path must also be bitwise identical across widths and bitwise
+equal to spmm_csr when the block part is empty (the contract of
+tests/aic_aiv_ablation/bitwise_correctness.py:138-175).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+TOL = {"fp16": 2e-2, "fp32": 1e-4}
+NP_DT = {"fp16": np.float16, "fp32": np.float32}
+
+
+def random_csr(rng, rows, cols, max_deg, long_rows=(), empty_frac=0.2):
+    """Distinct sorted columns per row; some empty rows; optional long rows."""
+    deg = rng.integers(0, max_deg + 1, size=rows)
+    deg[rng.random(rows) < empty_frac] = 0
+    for r, d in long_rows:
+        deg[r] = min(d, cols)
+    parts = [np.sort(rng.choice(cols, int(d), replace=False)) for d in deg]
+    crow = np.zeros(rows + 1, dtype=np.int64)
+    crow[1:] = np.cumsum(deg)
+    col = np.concatenate(parts).astype(np.int64) if parts else np.zeros(0, np.int64)
+    return crow, col
+
+
+def dev(a, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    if dtype is not None:
+        t = t.to(dtype)
+    return t.cuda()
+
+
+def zero_start(n):
+    return torch.zeros(n, dtype=torch.int32, device="cuda")
+
+
+def assert_close(actual, expected_f64, dtype):
+    tol = TOL[dtype]
+    a = actual.float().cpu().double()
+    e = torch.from_numpy(expected_f64)
+    close = torch.isclose(a, e, atol=tol, rtol=tol)
+    bad = int((~close).sum())
+    assert bad == 0, f"{bad} mismatches, max abs err {float((a - e).abs().max()):.3e}"
+
+
+def run_csr(spmm_npu, crow, col, vals, B, index_dtype=torch.int32):
+    return spmm_npu.spmm_csr(dev(crow, index_dtype), dev(col, index_dtype), dev(vals), dev(B),
+                             dev(O.make_start(crow, 40)))
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "fp32"])
+@pytest.mark.parametrize("width", [16, 32, 48, 64, 128, 256, 512])
+def test_spmm_csr_matches_oracle(spmm_npu, dtype, width):
+    rng = np.random.default_rng(100 + width)
+    crow, col = random_csr(rng, 300, 257, 40, long_rows=[(7, 200), (150, 257)])
+    vals = rng.uniform(-1, 1, col.size).astype(NP_DT[dtype])
+    B = rng.standard_normal((257, width)).astype(NP_DT[dtype])
+    out = run_csr(spmm_npu, crow, col, vals, B)
+    torch.cuda.synchronize()
+    assert out.shape == (300, width) and out.dtype == dev(vals).dtype
+    assert_close(out, O.spmm_f64(crow, col, vals, B), dtype)
+
+
+def test_spmm_csr_fp16_width_1024(spmm_npu):
+    rng = np.random.default_rng(7)
+    crow, col = random_csr(rng, 120, 90, 30, long_rows=[(3, 90)])
+    vals = rng.uniform(-1, 1, col.size).astype(np.float16)
+    B = rng.standard_normal((90, 1024)).astype(np.float16)
+    out = run_csr(spmm_npu, crow, col, vals, B)
+    assert_close(out, O.spmm_f64(crow, col, vals, B), "fp16")
+
+
+@pytest.mark.parametrize("index_dtype", [torch.int32, torch.int64])
+def test_spmm_csr_long_rows_cross_ranges(spmm_npu, index_dtype):
+    """Rows of 1000..5000 nonzeros cross many fixed ranges (fix-up path)."""
+    rng = np.random.default_rng(11)
+    crow, col = random_csr(rng, 64, 6000, 5, long_rows=[(0, 1000), (5, 5000), (6, 129), (63, 2500)])
+    vals = rng.uniform(-1, 1, col.size).astype(np.float32)
+    B = rng.standard_normal((6000, 64)).astype(np.float32)
+    out = run_csr(spmm_npu, crow, col, vals, B, index_dtype)
+    assert_close(out, O.spmm_f64(crow, col, vals, B), "fp32")
+
+
+def test_spmm_csr_edge_shapes(spmm_npu):
+    rng = np.random.default_rng(3)
+    B = rng.standard_normal((10, 16)).astype(np.float32)
+    # all rows empty (nnz = 0): zeros
+    crow = np.zeros(6, dtype=np.int64)
+    out = run_csr(spmm_npu, crow, np.zeros(0, np.int64), np.zeros(0, np.float32), B)
+    assert out.shape == (5, 16) and bool((out == 0).all())
+    # zero rows
+    out = run_csr(spmm_npu, np.zeros(1, np.int64), np.zeros(0, np.int64), np.zeros(0, np.float32), B)
+    assert out.shape == (0, 16)
+    # identity -> C == B exactly; single nnz per row -> exact scaled copy
+    crow = np.arange(11, dtype=np.int64)
+    col = np.arange(10, dtype=np.int64)
+    out = run_csr(spmm_npu, crow, col, np.ones(10, np.float32), B)
+    assert torch.equal(out.cpu(), torch.from_numpy(B))
+    Bh = B.astype(np.float16)
+    out = run_csr(spmm_npu, crow, col[::-1].copy(), np.full(10, 2.0, np.float16), Bh)
+    assert torch.equal(out.cpu(), torch.from_numpy((2 * Bh[::-1]).astype(np.float16)))
+
+
+def test_spmm_csr_matches_torch_sparse_cpu(spmm_npu):
+    """Against the reference's own CPU path (cpu_reference, torch CSR sparse.mm)."""
+    w = W.config1(scale=1 / 16)
+    B = w.dense(128)
+    out = run_csr(spmm_npu, w.crow, w.col, w.values, B)
+    ref = O.cpu_reference(w.rows, w.cols, w.crow, w.col, w.values, B)
+    close = torch.isclose(out.cpu(), ref, atol=1e-4, rtol=1e-4)
+    assert bool(close.all())
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "fp32"])
+def test_vector_path_width_invariant_bitwise(spmm_npu, dtype):
+    """C_maxwidth[:, :n] == C_n bit for bit for every width n."""
+    rng = np.random.default_rng(21)
+    crow, col = random_csr(rng, 200, 300, 25, long_rows=[(1, 300), (100, 260)])
+    vals = rng.uniform(-1, 1, col.size).astype(NP_DT[dtype])
+    maxw = 1024 if dtype == "fp16" else 512
+    B = rng.standard_normal((300, maxw)).astype(NP_DT[dtype])
+    full = run_csr(spmm_npu, crow, col, vals, B).cpu()
+    for n in (16, 32, 64, 128, 256, 512, 1024):
+        if n > maxw:
+            continue
+        part = run_csr(spmm_npu, crow, col, vals, np.ascontiguousarray(B[:, :n])).cpu()
+        assert torch.equal(part, full[:, :n]), f"width {n} differs"
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "fp32"])
+@pytest.mark.parametrize("width", [16, 128, 256])
+def test_mixed_with_empty_block_part_equals_csr_bitwise(spmm_npu, dtype, width):
+    rng = np.random.default_rng(31 + width)
+    crow, col = random_csr(rng, 333, 400, 30, long_rows=[(2, 400), (200, 390)])
+    vals = rng.uniform(-1, 1, col.size).astype(NP_DT[dtype])
+    B = rng.standard_normal((400, width)).astype(NP_DT[dtype])
+    ref = run_csr(spmm_npu, crow, col, vals, B)
+    i32 = torch.int32
+    mixed = spmm_npu.spmm_ascend_cube(
+        zero_start(1), torch.zeros(0, dtype=i32, device="cuda"),
+        torch.zeros(0, dtype=dev(vals).dtype, device="cuda"),
+        dev(crow, i32), dev(col, i32), dev(vals), dev(B), zero_start(20),
+        dev(O.make_start(crow, 40)))
+    assert torch.equal(mixed[:333].cpu(), ref.cpu())
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "fp32"])
+@pytest.mark.parametrize("width", [16, 64, 128, 192, 512])
+def test_block_part_from_bcsr(spmm_npu, dtype, width):
+    """Pure block part (csr_to_bcsr layout, empty vector part) vs fp64."""
+    rng = np.random.default_rng(41 + width)
+    crow, col = random_csr(rng, 250, 300, 60, long_rows=[(4, 300)])
+    vals = rng.uniform(-1, 1, col.size).astype(NP_DT[dtype])
+    B = rng.standard_normal((300, width)).astype(NP_DT[dtype])
+    b = O.csr_to_bcsr(crow, col, vals, 250, 300, 16)
+    i32 = torch.int32
+    for op in (spmm_npu.spmm_ascend_cube, spmm_npu.spmm_ascend_cube_aic_without_pipeline):
+        out = op(dev(b["crow_window_ptr"], i32), dev(b["unique_col_ids"], i32), dev(b["value"]),
+                 zero_start(1), torch.zeros(0, dtype=i32, device="cuda"),
+                 torch.zeros(0, dtype=dev(vals).dtype, device="cuda"), dev(B),
+                 dev(O.make_start(b["crow_window_ptr"], 20)), zero_start(40))
+        assert out.shape == (16 * 16, width)
+        assert_close(out[:250], O.spmm_f64(crow, col, vals, B), dtype)
+        assert bool((out[250:] == 0).all())
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "fp32"])
+def test_mixed_block_level_split(spmm_npu, dtype):
+    """block_level_split layout: BSR over all windows + CSR residual, original row order."""
+    rng = np.random.default_rng(51)
+    crow, col = random_csr(rng, 500, 500, 40, long_rows=[(9, 480)])
+    vals = rng.uniform(-1, 1, col.size).astype(NP_DT[dtype])
+    B = rng.standard_normal((500, 128)).astype(NP_DT[dtype])
+    h = O.block_level_split(crow, col, vals, 500, 500, (222.0 / 190.0) * 0.5, 16)
+    assert h["vcol_indices"].size > 0 and h["unique_col_ids"].size > 0
+    i32 = torch.int32
+    out = spmm_npu.spmm_ascend_cube(
+        dev(h["crow_window_ptr"], i32), dev(h["unique_col_ids"], i32), dev(h["value"]),
+        dev(h["vrow_window_ptr"], i32), dev(h["vcol_indices"], i32), dev(h["vvalue"]), dev(B),
+        dev(O.make_start(h["crow_window_ptr"], 20)), dev(O.make_start(h["vrow_window_ptr"], 40)))
+    assert_close(out[:500], O.spmm_f64(crow, col, vals, B), dtype)
+
+
+@pytest.mark.parametrize("graph_layout", [False, True])
+def test_mixed_preprocess_layout_unpermuted(spmm_npu, graph_layout):
+    """preprocess layout: packed rows; restore with inv_permutation before comparing
+    (the reference's task-mapping test omits this step, see its correctness.py:179-182)."""
+    rng = np.random.default_rng(61)
+    w = W.config4(scale=0.01)
+    B = w.dense(64)
+    p = O.preprocess(w.crow, w.col, w.values, w.rows, w.cols, 16, graph_layout)
+    i32 = torch.int32
+    ccol = p["renumbered_unique_col_ids"] if graph_layout else p["unique_col_ids"]
+    vcol = p["renumbered_vcol_indices"] if graph_layout else p["vcol_indices"]
+    dense = dev(B)
+    if graph_layout:
+        dense = spmm_npu.pack_node_tensor(dense, torch.from_numpy(p["inv_permutation"]),
+                                          int(p["packed_rows"][0]))
+    out = spmm_npu.spmm_ascend_cube(
+        dev(p["crow_window_ptr"], i32), dev(ccol, i32), dev(p["value"]),
+        dev(p["vrow_window_ptr"], i32), dev(vcol, i32), dev(p["vvalue"]), dense,
+        dev(O.make_start(p["crow_window_ptr"], 20)), dev(O.make_start(p["vrow_window_ptr"], 40)))
+    restored = spmm_npu.restore_node_tensor(out, torch.from_numpy(p["inv_permutation"]))
+    assert restored.shape == (w.rows, 64)
+    assert_close(restored, O.spmm_f64(w.crow, w.col, w.values, B), "fp16")
+    del rng
+
+
+def test_results_are_deterministic(spmm_npu):
+    w = W.config2(scale=0.05)
+    B = w.dense(128)
+    a = run_csr(spmm_npu, w.crow, w.col, w.values, B).cpu()
+    b = run_csr(spmm_npu, w.crow, w.col, w.values, B).cpu()
+    assert torch.equal(a, b)
+
+
+def test_aliases_match_base_ops(spmm_npu):
+    rng = np.random.default_rng(71)
+    crow, col = random_csr(rng, 100, 100, 20)
+    vals = rng.uniform(-1, 1, col.size).astype(np.float16)
+    B = rng.standard_normal((100, 64)).astype(np.float16)
+    args = (dev(crow, torch.int32), dev(col, torch.int32), dev(vals), dev(B),
+            dev(O.make_start(crow, 40)))
+    assert torch.equal(spmm_npu.spmm_csr(*args), spmm_npu.spmm_csr_aiv_mb_batch(*args))
+    i32 = torch.int32
+    margs = (zero_start(1), torch.zeros(0, dtype=i32, device="cuda"),
+             torch.zeros(0, dtype=torch.float16, device="cuda"), args[0], args[1], args[2],
+             args[3], zero_start(20), args[4])
+    assert torch.equal(spmm_npu.spmm_ascend_cube(*margs), spmm_npu.spmm_ascend_cube_aiv_mb(*margs))
+
+
+def test_contract_errors(spmm_npu):
+    i32 = torch.int32
+    crow = dev(np.array([0, 1], np.int64), i32)
+    col = dev(np.array([0], np.int64), i32)
+    v = torch.ones(1, dtype=torch.float16, device="cuda")
+    st = zero_start(40)
+    with pytest.raises(RuntimeError, match="feature width divisible by 16"):
+        spmm_npu.spmm_csr(crow, col, v, torch.ones(2, 24, dtype=torch.float16, device="cuda"), st)
+    with pytest.raises(RuntimeError, match="0 < feature width <= 1024 for FP16"):
+        spmm_npu.spmm_csr(crow, col, v, torch.ones(2, 1040, dtype=torch.float16, device="cuda"), st)
+    with pytest.raises(RuntimeError, match="0 < feature width <= 512 for FP32"):
+        spmm_npu.spmm_csr(crow, col, v.float(), torch.ones(2, 520, device="cuda"), st)
+    with pytest.raises(RuntimeError, match="must have the same dtype as dense"):
+        spmm_npu.spmm_csr(crow, col, v, torch.ones(2, 16, device="cuda"), st)
+    with pytest.raises(RuntimeError, match="col and value must be same size"):
+        spmm_npu.spmm_csr(crow, col, torch.ones(2, dtype=torch.float16, device="cuda"),
+                          torch.ones(2, 16, dtype=torch.float16, device="cuda"), st)
+    with pytest.raises(RuntimeError, match="must be a GPU tensor"):
+        spmm_npu.spmm_csr(crow.cpu(), col, v, torch.ones(2, 16, dtype=torch.float16, device="cuda"), st)
+    # fp32 spmm_csr accepts widths divisible by 8 (extension/custom_op.cpp:78)
+    out = spmm_npu.spmm_csr(crow, col, v.float(), torch.ones(2, 24, device="cuda"), st)
+    assert torch.equal(out.cpu(), torch.ones(1, 24))
+
+
+def test_out_of_range_columns_contribute_zero(spmm_npu):
+    """Column ids outside dense are skipped by the kernels (no out-of-bounds read)."""
+    crow = np.array([0, 2, 3], np.int64)
+    col = np.array([1, 99, 0], np.int64)
+    vals = np.array([1.0, 5.0, 2.0], np.float32)
+    B = np.arange(32, dtype=np.float32).reshape(2, 16)
+    out = run_csr(spmm_npu, crow, col, vals, B).cpu().numpy()
+    np.testing.assert_array_equal(out, np.stack([B[1], 2 * B[0]]))
+
+
+def test_pack_restore_match_oracle(spmm_npu):
+    rng = np.random.default_rng(81)
+    x = rng.standard_normal((50, 24)).astype(np.float32)
+    inv = rng.permutation(64)[:50].astype(np.int64)
+    packed = spmm_npu.pack_node_tensor(dev(x), torch.from_numpy(inv), 64)
+    np.testing.assert_array_equal(packed.cpu().numpy(), O.pack_node_tensor(x, inv, 64))
+    back = spmm_npu.restore_node_tensor(packed, torch.from_numpy(inv))
+    np.testing.assert_array_equal(back.cpu().numpy(), x)
+    # odd row size (3 bytes per row) takes the byte path
+    xb = rng.integers(0, 255, size=(50, 3)).astype(np.uint8)
+    pb = spmm_npu.pack_node_tensor(dev(xb), torch.from_numpy(inv))
+    np.testing.assert_array_equal(pb.cpu().numpy(), O.pack_node_tensor(xb, inv))
+    with pytest.raises(ValueError, match="packed_rows is smaller"):
+        spmm_npu.pack_node_tensor(dev(x), torch.from_numpy(inv), 10)
+    with pytest.raises(ValueError, match="invalid packed node id"):
+        spmm_npu.restore_node_tensor(packed[:10], torch.from_numpy(inv))
+
+
+def test_config2_full_size_matches_oracle(spmm_npu):
+    """BASELINE config 2 at full size (power-law, fp16, N=128) vs the fp64 oracle."""
+    w = W.config2()
+    B = w.dense(128)
+    out = run_csr(spmm_npu, w.crow, w.col, w.values, B)
+    assert_close(out, O.spmm_f64(w.crow, w.col, w.values, B), "fp16")
