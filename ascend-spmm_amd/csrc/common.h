@@ -31,11 +31,14 @@ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
-// Split length of the CSR gather path: nonzeros are cut into ranges of this
-// many positions (relative to the first nonzero of the vector rows).  It is a
-// constant of the library, independent of width and dtype, which is what makes
-// the gather results identical for every feature width.
-constexpr int64_t kGatherRange = 128;
+// Split length of the CSR gather path: nonzero positions are cut into ranges
+// [j*R, (j+1)*R).  It is a constant of the build, independent of width and
+// dtype, which is what makes the gather results identical for every feature
+// width.
+#ifndef SPMM_GATHER_RANGE
+#define SPMM_GATHER_RANGE 256
+#endif
+constexpr int64_t kGatherRange = SPMM_GATHER_RANGE;
 
 // fp32 storage of one partial row in the gather workspace, padded so every
 // slot starts 256-byte aligned.

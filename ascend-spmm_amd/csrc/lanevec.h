@@ -11,10 +11,23 @@ namespace lanes {
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 
+typedef unsigned int raw16_t __attribute__((ext_vector_type(4)));
+
+// Raw 16-byte load (converted later, so the load can be issued early).
+template <typename T>
+__device__ inline raw16_t load_raw16(const T* p) {
+  return *reinterpret_cast<const raw16_t*>(p);
+}
+
 // Elements per lane: 16 bytes of the value type.
 template <typename T> struct LaneVec;
 template <> struct LaneVec<_Float16> {
   static constexpr int V = 8;
+  __device__ static inline void unpack(const raw16_t& r, float* f) {
+    half8_t h = __builtin_bit_cast(half8_t, r);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[i] = static_cast<float>(h[i]);
+  }
   __device__ static inline void load(const _Float16* p, float* f) {
     half8_t h = *reinterpret_cast<const half8_t*>(p);
 #pragma unroll
@@ -29,6 +42,11 @@ template <> struct LaneVec<_Float16> {
 };
 template <> struct LaneVec<float> {
   static constexpr int V = 4;
+  __device__ static inline void unpack(const raw16_t& r, float* f) {
+    float4_t v = __builtin_bit_cast(float4_t, r);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) f[i] = v[i];
+  }
   __device__ static inline void load(const float* p, float* f) {
     float4_t v = *reinterpret_cast<const float4_t*>(p);
 #pragma unroll

@@ -55,6 +55,13 @@ spmm_status check_width(int64_t width, int32_t value_type, int64_t alignment, co
   return SPMM_OK;
 }
 
+// The kernels move 16-byte (gather) / 8-byte (block) pieces of dense and out.
+spmm_status check_aligned(const void* dense, const void* out, const char* op) {
+  if ((reinterpret_cast<uintptr_t>(dense) | reinterpret_cast<uintptr_t>(out)) % 16 != 0)
+    return fail(SPMM_ERR_CONTRACT, std::string(op) + ": dense and out must be 16-byte aligned");
+  return SPMM_OK;
+}
+
 }  // namespace
 }  // namespace spmm
 
@@ -89,6 +96,7 @@ spmm_status spmm_csr_run(const spmm_csr_desc* d, const void* rowptr, const void*
   if (rowptr == nullptr || out == nullptr || (d->nnz > 0 && (col == nullptr || value == nullptr)) ||
       (d->dense_rows > 0 && dense == nullptr))
     return fail(SPMM_ERR_INVALID_ARGUMENT, "spmm_csr: null device pointer");
+  if (spmm_status st = check_aligned(dense, out, "spmm_csr")) return st;
   return launch_gather(d->index_type, d->value_type, rowptr, col, value, d->nnz, 0, d->rows,
                        dense, d->dense_rows, d->width, out, workspace, workspace_bytes,
                        as_stream(stream));
@@ -128,6 +136,7 @@ spmm_status spmm_mixed_run(const spmm_mixed_desc* d, const void* Crowptr, const 
       (d->vector_rows > 0 && Vrowptr == nullptr) ||
       (d->vector_nnz > 0 && (Vcol == nullptr || Vvalue == nullptr)))
     return fail(SPMM_ERR_INVALID_ARGUMENT, "spmm_ascend_cube: null device pointer");
+  if (spmm_status st = check_aligned(dense, out, "spmm_ascend_cube")) return st;
   hipStream_t s = as_stream(stream);
   const int64_t block_rows = 16 * d->block_windows;
   spmm_status st =

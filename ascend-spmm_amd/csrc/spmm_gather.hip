@@ -7,19 +7,26 @@
 // accumulated in fp32 and rounded once to the output type.
 //
 // Work decomposition (MI355X-native, not the reference's 40-core split):
-//  * The nonzero positions are cut into fixed ranges of kGatherRange
-//    positions ([j*kGatherRange, (j+1)*kGatherRange)).  A "lane group" of
-//    L lanes (L = width / 8 for fp16, width / 4 for fp32, capped at 64; each
-//    lane owns 16 bytes of an output row) processes one range.
-//  * A row that lies inside one range is accumulated sequentially by that
-//    group and written directly.  A row that crosses range ends leaves one
-//    fp32 partial per range in the workspace ("tail" in the range where it
-//    starts, "head" in each later range); the fix-up kernel adds them in range
-//    order.  Cut points depend only on the row pointer, so every output element
-//    has the same operation sequence for every width N: results are
-//    deterministic and bit-identical across widths.
-//  * The dense row gather is a 16-byte load per lane; the L lanes of a group
-//    read L*16 contiguous bytes of one dense row (coalesced).
+//  * Nonzero positions are cut into fixed ranges [j*R, (j+1)*R) with
+//    R = kGatherRange.  A "lane group" of L lanes (each lane owns 16 bytes of
+//    an output row: L = width/8 for fp16, width/4 for fp32, capped at 64)
+//    processes one range.  Cut points depend only on the positions, so every
+//    output element sees the same fp32 operation sequence for every width N:
+//    results are deterministic and bit-identical across widths.
+//  * gather_tiles: a work-group takes a tile of consecutive ranges.  It finds
+//    the rows starting in the tile with a work-group-wide many-way search of
+//    the row pointer (a few rounds of one load per thread instead of a chain
+//    of dependent loads), stages the tile's column ids and values in LDS and
+//    marks, per position, the row that starts there.  Each lane group then
+//    streams its range flat: the dense rows of 8 consecutive nonzeros are
+//    loaded together, two batches in flight (16 bytes per lane; the L lanes
+//    of a group read L*16 contiguous bytes of one dense row), accumulated in
+//    order, and flushed wherever the next position starts a new row.  Empty
+//    rows are written as zeros.
+//  * A row that crosses range ends leaves one fp32 partial per range in the
+//    workspace ("tail" in the range where it starts, "head" in every later
+//    range) and its id in the range's tail entry; gather_fixup adds the
+//    partials in range order.
 #include "common.h"
 #include "lanevec.h"
 
@@ -27,20 +34,24 @@ namespace spmm {
 namespace {
 
 using lanes::LaneVec;
-using lanes::accumulate;
 using lanes::clampi;
 
-// Geometry shared by the main and fix-up kernels.  Ranges are absolute
-// positions [j*kGatherRange, (j+1)*kGatherRange) of the nonzero arrays, so the
-// host needs only the array extent (no read-back of the row pointer).
+constexpr int kWgThreads = 256;
+#ifndef SPMM_GATHER_BATCH
+#define SPMM_GATHER_BATCH 8
+#endif
+constexpr int kBatch = SPMM_GATHER_BATCH;  // dense rows per batch (two batches in flight)
+constexpr int kStageUnroll = 8;             // staging loads issued per thread before storing
+constexpr int64_t kTilePositions = 4096;    // nonzeros staged per work-group
+
 template <typename I>
-struct Ranges {
+struct Geometry {
   const I* rowptr;
+  int64_t* tail;           // [nranges]: row that starts in range j and runs past its end, or -1
   int64_t row_lo, row_hi;  // vector rows handled
   int64_t nnz;             // extent of col[] / value[]
-  int64_t nranges;         // max(1, ceil(nnz / kGatherRange))
+  int64_t nranges;         // max(1, ceil(nnz / R))
 
-  // Row pointer clamped into [0, nnz] so no position leaves the arrays.
   __device__ inline int64_t rp(int64_t r) const {
     return clampi(static_cast<int64_t>(rowptr[r]), 0, nnz);
   }
@@ -49,77 +60,295 @@ struct Ranges {
     const int64_t h = (j + 1) * kGatherRange;
     return h < nnz ? h : nnz;
   }
-  // First row r in [row_lo, row_hi] with rp(r) >= pos.
-  __device__ inline int64_t lower_row(int64_t pos) const {
-    int64_t a = row_lo, b = row_hi;
-    while (a < b) {
-      int64_t m = a + ((b - a) >> 1);
-      if (rp(m) < pos) a = m + 1; else b = m;
-    }
-    return a;
-  }
-  __device__ inline int64_t row_begin(int64_t j) const { return j == 0 ? row_lo : lower_row(lo(j)); }
-  __device__ inline int64_t row_end(int64_t j) const { return j == nranges - 1 ? row_hi : lower_row(lo(j + 1)); }
 };
 
-// One lane group per (range j, column chunk cc).
+// Work-group search: first row r in [row_lo, row_hi] with rp(r) >= pos (row_hi
+// if none), for two positions at once (one per half of the work-group).  Each
+// round probes `half` evenly spaced rows and keeps the bracket of the first
+// hit, so a 100k-row pointer takes three rounds of one load per thread instead
+// of a 17-step chain of dependent loads.
+template <typename I>
+__device__ inline void wg_lower_rows(const Geometry<I>& g, int64_t posA, int64_t posB,
+                                     int64_t& outA, int64_t& outB) {
+  __shared__ int s_min[2];
+  __shared__ int64_t s_ans[2];
+  const int half = blockDim.x >> 1;
+  const int q = threadIdx.x >= half ? 1 : 0;
+  const int k = threadIdx.x - q * half;
+  const int64_t pos = q ? posB : posA;
+  int64_t lo = g.row_lo, hi = g.row_hi;
+  bool done = false;
+  for (int round = 0; round < 12; ++round) {
+    if (threadIdx.x < 2) s_min[threadIdx.x] = INT32_MAX;
+    __syncthreads();
+    const int64_t n = hi - lo;
+    const bool final_round = n <= half;
+    if (!done) {
+      const int64_t r = final_round ? lo + k : lo + (n * (k + 1)) / (half + 1);
+      if ((!final_round || k < n) && g.rp(r) >= pos) atomicMin(&s_min[q], k);
+    }
+    __syncthreads();
+    if (!done) {
+      const int km = s_min[q];
+      if (final_round) {
+        if (km != INT32_MAX) hi = lo + km;
+        done = true;
+      } else if (km == INT32_MAX) {
+        lo = lo + (n * half) / (half + 1) + 1;
+      } else {
+        const int64_t rk = lo + (n * (km + 1)) / (half + 1);
+        lo = km == 0 ? lo : lo + (n * km) / (half + 1) + 1;
+        hi = rk;
+      }
+    }
+    if (__syncthreads_and(done)) break;
+  }
+  if (k == 0) s_ans[q] = hi;
+  __syncthreads();
+  outA = s_ans[0];
+  outB = s_ans[1];
+}
+
+// One batch of kBatch consecutive nonzeros: raw 16-byte dense pieces, values
+// and column validity.
+template <typename T>
+struct Batch {
+  lanes::raw16_t x[kBatch];
+  float v[kBatch];
+  bool ok[kBatch];
+};
+
+// Issues the dense loads of a batch from the LDS-staged column ids.
 template <typename T, typename I>
-__global__ __launch_bounds__(256) void gather_main(Ranges<I> g, const I* __restrict__ col,
-                                                   const T* __restrict__ value,
-                                                   const T* __restrict__ dense, int64_t K,
-                                                   int64_t N, T* __restrict__ out,
-                                                   float* __restrict__ ws, int log2L,
-                                                   int64_t chunks, int64_t slot) {
+struct Stream {
+  const I* s_col;
+  const T* s_val;
+  const T* dense;
+  int64_t K, N, c0, P0, pe;
+
+  // Branch-free so the loads of a batch stay in flight together: positions
+  // past the range end and invalid columns load dense row 0 (K >= 1 here)
+  // and are masked out by `ok`.
+  __device__ inline void issue(Batch<T>& b, int64_t p0) const {
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int64_t p = p0 + u;
+      const int64_t q = (p < pe ? p : pe - 1) - P0;
+      const int64_t c = static_cast<int64_t>(s_col[q]);
+      b.v[u] = static_cast<float>(s_val[q]);
+      b.ok[u] = p < pe && static_cast<uint64_t>(c) < static_cast<uint64_t>(K);
+      b.x[u] = lanes::load_raw16(dense + (b.ok[u] ? c : 0) * N + c0);
+    }
+  }
+};
+
+// Accumulates batches in position order.  Per tile position the LDS mark is
+// (row + 1 - tA) << 1 | ends_here, where the row part is set only at the
+// position a row starts: it tracks the current row and flushes at row ends.
+template <typename T>
+struct Sink {
+  const int32_t* s_mark;
+  int64_t P0, pe, tA, row_hi;
+  T* out;
+  int64_t N, c0;
+  float* head_slot;
+  float* tail_slot;
+  int64_t row;             // row in progress, -1 while it is one started before the range
+  bool last_ended;         // the last consumed position ended its row
+  float acc[lanes::LaneVec<T>::V];
+
+  __device__ inline void consume(const Batch<T>& b, int64_t p0) {
+    constexpr int V = lanes::LaneVec<T>::V;
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int64_t p = p0 + u;
+      if (p < pe) {
+        const int32_t m = s_mark[p - P0];
+        if (m >> 1) row = tA + (m >> 1) - 1;
+        float x[V];
+        lanes::LaneVec<T>::unpack(b.x[u], x);
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+          const float t = __builtin_fmaf(b.v[u], x[i], acc[i]);
+          acc[i] = b.ok[u] ? t : acc[i];
+        }
+        last_ended = m & 1;
+        if (last_ended) {
+          if (row < 0) {
+#pragma unroll
+            for (int i = 0; i < V; ++i) head_slot[i] = acc[i];
+          } else if (row < row_hi) {
+            lanes::LaneVec<T>::store(out + row * N + c0, acc);
+          }
+#pragma unroll
+          for (int i = 0; i < V; ++i) acc[i] = 0.f;
+        }
+      }
+    }
+  }
+
+  // The row in progress at the range end continues into the next range:
+  // returns that row if it started in this range (a tail), else -1.
+  __device__ inline int64_t finish() {
+    constexpr int V = lanes::LaneVec<T>::V;
+    if (last_ended) return -1;
+    float* dst = row < 0 ? head_slot : tail_slot;
+#pragma unroll
+    for (int i = 0; i < V; ++i) dst[i] = acc[i];
+    return row;
+  }
+};
+
+template <typename T, typename I>
+__global__ __launch_bounds__(kWgThreads) void gather_tiles(
+    Geometry<I> g, const I* __restrict__ col, const T* __restrict__ value,
+    const T* __restrict__ dense, int64_t K, int64_t N, T* __restrict__ out, float* __restrict__ ws,
+    int log2L, int64_t chunks, int64_t ranges_per_tile, int64_t slot) {
   constexpr int V = LaneVec<T>::V;
-  const int L = 1 << log2L;
-  const int64_t tid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  const int64_t item = tid >> log2L;
-  const int lane = static_cast<int>(tid & (L - 1));
-  if (item >= g.nranges * chunks) return;
-  const int64_t j = item / chunks;
-  const int64_t cc = item - j * chunks;
-  const int64_t c0 = (cc * L + lane) * V;
-  if (c0 >= N) return;
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int64_t tile_positions = ranges_per_tile * kGatherRange;
+  I* s_col = reinterpret_cast<I*>(smem);
+  T* s_val = reinterpret_cast<T*>(smem + tile_positions * sizeof(I));
+  int32_t* s_mark = reinterpret_cast<int32_t*>(smem + tile_positions * (sizeof(I) + sizeof(T)));
 
-  const int64_t plo = g.lo(j), phi = g.hi(j);
-  const int64_t rb = g.row_begin(j), re = g.row_end(j);
+  const int64_t j0 = static_cast<int64_t>(blockIdx.x) * ranges_per_tile;
+  const int64_t j1 = (j0 + ranges_per_tile < g.nranges) ? j0 + ranges_per_tile : g.nranges;
+  const int64_t P0 = g.lo(j0), P1 = g.hi(j1 - 1);
+  const bool last_tile = j1 == g.nranges;
+  const int64_t base = g.rp(g.row_lo), end = g.rp(g.row_hi);
 
-  // Head: positions [plo, ...) of a row that started in an earlier range.
-  if (j > 0 && rb > g.row_lo) {
-    const int64_t stop = g.rp(rb);
-    if (stop > plo) {
-      float acc[V];
+  // Rows starting in the tile: [tA, rB) (rB = first row starting at or after P1).
+  int64_t tA, rB;
+  wg_lower_rows(g, P0, P1, tA, rB);
+  if (last_tile) rB = g.row_hi;
+
+  // Stage the tile's nonzeros of our rows ([base, end)) and clear the marks;
+  // each thread issues its loads before the first LDS store.
+  const bool any = base < end && P0 < end && P1 > base;  // uniform over the work-group
+  for (int64_t i0 = 0; i0 < tile_positions; i0 += kStageUnroll * blockDim.x) {
+    I cs[kStageUnroll];
+    T vs[kStageUnroll];
+    if (any) {
 #pragma unroll
-      for (int i = 0; i < V; ++i) acc[i] = 0.f;
-      accumulate<T, I>(acc, plo, stop < phi ? stop : phi, col, value, dense, K, N, c0);
-      float* dst = ws + (2 * j) * slot + c0;
+      for (int k = 0; k < kStageUnroll; ++k) {
+        int64_t p = P0 + i0 + k * blockDim.x + threadIdx.x;
+        p = p < base ? base : (p >= end ? end - 1 : p);
+        cs[k] = col[p];
+        vs[k] = value[p];
+      }
+    }
 #pragma unroll
-      for (int i = 0; i < V; ++i) dst[i] = acc[i];
+    for (int k = 0; k < kStageUnroll; ++k) {
+      const int64_t i = i0 + k * blockDim.x + threadIdx.x;
+      const int64_t p = P0 + i;
+      if (i < tile_positions) {
+        s_mark[i] = 0;
+        if (any && p >= base && p < end) {
+          s_col[i] = cs[k];
+          s_val[i] = vs[k];
+        }
+      }
     }
   }
-  for (int64_t r = rb; r < re; ++r) {
+  __syncthreads();
+  // Mark the starts and ends of the tile's non-empty rows (each position is
+  // marked only by the row that holds it; row tA-1 may start before the tile
+  // and end in it).  Write the empty rows the tile owns (those whose start
+  // lies in the tile, or at/after it for the last tile).
+  const int64_t r0 = tA - 1 > g.row_lo ? tA - 1 : g.row_lo;
+  for (int64_t r = r0 + threadIdx.x; r < rB; r += blockDim.x) {
     const int64_t a = g.rp(r), b = g.rp(r + 1);
-    float acc[V];
+    if (a < b) {
+      const bool start_in = a >= P0 && a < P1 && r >= tA && r - tA < INT32_MAX - 1;
+      const bool end_in = b - 1 >= P0 && b - 1 < P1;
+      if (start_in) s_mark[a - P0] = static_cast<int32_t>((r - tA + 1) << 1) | (end_in && b - 1 == a ? 1 : 0);
+      if (end_in && !(start_in && b - 1 == a)) s_mark[b - 1 - P0] = 1;
+    } else if (r >= tA && a >= P0 && (a < P1 || last_tile)) {
+      T* dst = out + r * N;
+      for (int64_t c = 0; c < N; c += V) {
+        float z[V];
 #pragma unroll
-    for (int i = 0; i < V; ++i) acc[i] = 0.f;
-    if (b <= phi) {
-      accumulate<T, I>(acc, a, b, col, value, dense, K, N, c0);
-      LaneVec<T>::store(out + r * N + c0, acc);
-    } else {
-      // Tail: the row continues into the next range.
-      accumulate<T, I>(acc, a, phi, col, value, dense, K, N, c0);
-      float* dst = ws + (2 * j + 1) * slot + c0;
-#pragma unroll
-      for (int i = 0; i < V; ++i) dst[i] = acc[i];
+        for (int i = 0; i < V; ++i) z[i] = 0.f;
+        LaneVec<T>::store(dst + c, z);
+      }
     }
   }
+  __syncthreads();
+
+  // Lane group -> (range j, column chunk cc).
+  const int L = 1 << log2L;
+  const int group = threadIdx.x >> log2L;
+  const int lane = threadIdx.x & (L - 1);
+  const int64_t j = j0 + group / chunks;
+  const int64_t cc = group % chunks;
+  if (j >= j1) return;
+  const bool reporter = lane == 0 && cc == 0;  // writes tail[j]
+  const int64_t c0 = (cc * L + lane) * V;
+  const int64_t lo = g.lo(j), hi = g.hi(j);
+  const int64_t ps = lo > base ? lo : base;
+  const int64_t pe = hi < end ? hi : end;
+  if (ps >= pe || c0 >= N) {
+    if (reporter) g.tail[j] = -1;
+    return;
+  }
+
+  Sink<T> sk;
+  sk.s_mark = s_mark;
+  sk.P0 = P0;
+  sk.pe = pe;
+  sk.tA = tA;
+  sk.row_hi = g.row_hi;
+  sk.last_ended = false;
+  sk.out = out;
+  sk.N = N;
+  sk.c0 = c0;
+  sk.head_slot = ws + (2 * j) * slot + c0;
+  sk.tail_slot = ws + (2 * j + 1) * slot + c0;
+  sk.row = -1;  // set by the first row-start mark; stays -1 for a row begun earlier
+#pragma unroll
+  for (int i = 0; i < V; ++i) sk.acc[i] = 0.f;
+
+  int64_t tail_row;
+  if (K <= 0) {  // no valid column: rows still flush (as zeros)
+    Batch<T> z;
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      z.ok[u] = false;
+      z.v[u] = 0.f;
+      z.x[u] = lanes::raw16_t{0, 0, 0, 0};
+    }
+    for (int64_t p0 = ps; p0 < pe; p0 += kBatch) sk.consume(z, p0);
+    tail_row = sk.finish();
+  } else {
+    // Two batches of kBatch dense rows in flight: the loads of batch k+1 are
+    // issued before batch k is accumulated.
+    Stream<T, I> st;
+    st.s_col = s_col;
+    st.s_val = s_val;
+    st.dense = dense;
+    st.K = K;
+    st.N = N;
+    st.c0 = c0;
+    st.P0 = P0;
+    st.pe = pe;
+    Batch<T> ba, bb;
+    st.issue(ba, ps);
+    for (int64_t p0 = ps; p0 < pe; p0 += 2 * kBatch) {
+      st.issue(bb, p0 + kBatch);
+      sk.consume(ba, p0);
+      st.issue(ba, p0 + 2 * kBatch);
+      sk.consume(bb, p0 + kBatch);
+    }
+    tail_row = sk.finish();
+  }
+  if (reporter) g.tail[j] = tail_row;
 }
 
 // Adds the partials of every row that crosses range ends, in range order.
 template <typename T, typename I>
-__global__ __launch_bounds__(256) void gather_fixup(Ranges<I> g, int64_t N, T* __restrict__ out,
-                                                    const float* __restrict__ ws, int log2L,
-                                                    int64_t chunks, int64_t slot) {
+__global__ __launch_bounds__(kWgThreads) void gather_fixup(Geometry<I> g, int64_t N, T* __restrict__ out,
+                                                           const float* __restrict__ ws, int log2L,
+                                                           int64_t chunks, int64_t slot) {
   constexpr int V = LaneVec<T>::V;
   const int L = 1 << log2L;
   const int64_t tid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -131,20 +360,38 @@ __global__ __launch_bounds__(256) void gather_fixup(Ranges<I> g, int64_t N, T* _
   const int64_t c0 = (cc * L + lane) * V;
   if (c0 >= N) return;
 
-  const int64_t rb = g.row_begin(j), re = g.row_end(j);
-  if (re <= rb) return;
-  const int64_t r = re - 1;
+  const int64_t r = g.tail[j];
+  if (r < g.row_lo || r >= g.row_hi) return;  // no row starts in range j and continues
   const int64_t stop = g.rp(r + 1);
-  if (stop <= g.hi(j)) return;  // last row of range j ends inside it
 
   float acc[V];
   const float* src = ws + (2 * j + 1) * slot + c0;
 #pragma unroll
   for (int i = 0; i < V; ++i) acc[i] = src[i];
-  for (int64_t k = j + 1; k < g.nranges && g.lo(k) < stop; ++k) {
-    const float* h = ws + (2 * k) * slot + c0;
+  // Head partials of ranges j+1 .. k_end-1, read 8 at a time, added in order.
+  int64_t k_end = (stop + kGatherRange - 1) / kGatherRange;
+  if (k_end > g.nranges) k_end = g.nranges;
+  constexpr int kFix = 8;
+  for (int64_t k0 = j + 1; k0 < k_end; k0 += kFix) {
+    lanes::raw16_t h[kFix][(V * 4 + 15) / 16];
 #pragma unroll
-    for (int i = 0; i < V; ++i) acc[i] = acc[i] + h[i];
+    for (int u = 0; u < kFix; ++u) {
+      const int64_t k = k0 + u < k_end ? k0 + u : k_end - 1;
+      const float* hp = ws + (2 * k) * slot + c0;
+#pragma unroll
+      for (int w = 0; w < (V * 4 + 15) / 16; ++w) h[u][w] = lanes::load_raw16(hp + 4 * w);
+    }
+#pragma unroll
+    for (int u = 0; u < kFix; ++u) {
+      if (k0 + u < k_end) {
+#pragma unroll
+        for (int w = 0; w < (V * 4 + 15) / 16; ++w) {
+          const lanes::float4_t f = __builtin_bit_cast(lanes::float4_t, h[u][w]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[4 * w + i] = acc[4 * w + i] + f[i];
+        }
+      }
+    }
   }
   LaneVec<T>::store(out + r * N + c0, acc);
 }
@@ -155,7 +402,7 @@ spmm_status gather_typed(const void* rowptr, const void* col, const void* value,
                          int64_t N, void* out, void* ws, size_t ws_bytes, hipStream_t stream) {
   constexpr int V = LaneVec<T>::V;
   if (row_hi <= row_lo) return SPMM_OK;
-  Ranges<I> g;
+  Geometry<I> g;
   g.rowptr = static_cast<const I*>(rowptr);
   g.row_lo = row_lo;
   g.row_hi = row_hi;
@@ -167,24 +414,37 @@ spmm_status gather_typed(const void* rowptr, const void* col, const void* value,
   while ((1 << log2L) < lanes_needed && log2L < 6) ++log2L;
   const int L = 1 << log2L;
   const int64_t chunks = ceil_div(lanes_needed, L);
+  // A tile stages at most kTilePositions nonzeros (LDS <= 64 KB).
+  int64_t ranges_per_tile = (kWgThreads / L) / chunks;
+  if (ranges_per_tile * kGatherRange > kTilePositions) ranges_per_tile = kTilePositions / kGatherRange;
+  if (ranges_per_tile < 1) ranges_per_tile = 1;
+  const int64_t groups_per_wg = ranges_per_tile * chunks;
+  const int64_t wg_threads = groups_per_wg * L;
   const int64_t slot = gather_slot_floats(N);
-  const size_t need = static_cast<size_t>(2 * g.nranges) * slot * sizeof(float);
-  if (g.nranges > 1 && (ws == nullptr || ws_bytes < need))
+
+  // Workspace: tail rows, then the partial slots (256-byte aligned).
+  const size_t tail_bytes = align_up(static_cast<size_t>(g.nranges) * sizeof(int64_t), 256);
+  const size_t need = tail_bytes + static_cast<size_t>(2 * g.nranges) * slot * sizeof(float);
+  if (ws == nullptr || ws_bytes < need)
     return fail(SPMM_ERR_CONTRACT, "gather workspace too small: need " + std::to_string(need) +
                                        " bytes, got " + std::to_string(ws_bytes));
+  g.tail = static_cast<int64_t*>(ws);
+  float* partial = reinterpret_cast<float*>(static_cast<char*>(ws) + tail_bytes);
 
-  const int64_t threads = g.nranges * chunks * L;
-  const int64_t blocks = ceil_div(threads, 256);
-  hipLaunchKernelGGL((gather_main<T, I>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
-                     g, static_cast<const I*>(col), static_cast<const T*>(value),
-                     static_cast<const T*>(dense), K, N, static_cast<T*>(out),
-                     static_cast<float*>(ws), log2L, chunks, slot);
-  spmm_status st = check_launch("gather_main");
+  const int64_t tiles = ceil_div(g.nranges, ranges_per_tile);
+  const size_t lds = static_cast<size_t>(ranges_per_tile * kGatherRange) *
+                     (sizeof(I) + sizeof(T) + sizeof(int32_t));
+  hipLaunchKernelGGL((gather_tiles<T, I>), dim3(static_cast<unsigned>(tiles)),
+                     dim3(static_cast<unsigned>(wg_threads)), lds, stream, g,
+                     static_cast<const I*>(col), static_cast<const T*>(value),
+                     static_cast<const T*>(dense), K, N, static_cast<T*>(out), partial, log2L,
+                     chunks, ranges_per_tile, slot);
+  spmm_status st = check_launch("gather_tiles");
   if (st != SPMM_OK || g.nranges < 2) return st;
   const int64_t fthreads = (g.nranges - 1) * chunks * L;
-  hipLaunchKernelGGL((gather_fixup<T, I>), dim3(static_cast<unsigned>(ceil_div(fthreads, 256))),
-                     dim3(256), 0, stream, g, N, static_cast<T*>(out),
-                     static_cast<const float*>(ws), log2L, chunks, slot);
+  hipLaunchKernelGGL((gather_fixup<T, I>), dim3(static_cast<unsigned>(ceil_div(fthreads, kWgThreads))),
+                     dim3(kWgThreads), 0, stream, g, N, static_cast<T*>(out),
+                     static_cast<const float*>(partial), log2L, chunks, slot);
   return check_launch("gather_fixup");
 }
 
@@ -192,7 +452,8 @@ spmm_status gather_typed(const void* rowptr, const void* col, const void* value,
 
 size_t gather_workspace_bytes(int64_t nnz, int64_t width) {
   const int64_t nr = (nnz > 0 ? ceil_div(nnz, kGatherRange) : 1);
-  return static_cast<size_t>(2 * nr) * gather_slot_floats(width) * sizeof(float);
+  return align_up(static_cast<size_t>(nr) * sizeof(int64_t), 256) +
+         static_cast<size_t>(2 * nr) * gather_slot_floats(width) * sizeof(float);
 }
 
 spmm_status launch_gather(int32_t index_type, int32_t value_type, const void* rowptr,

@@ -80,6 +80,11 @@ void check_same_device(const at::Tensor& a, const at::Tensor& b, const char* nam
   TORCH_CHECK(a.device() == b.device(), name, " must be on the same device as dense");
 }
 
+// The kernels read dense in 16-byte pieces; a view at an odd offset is copied.
+at::Tensor aligned(const at::Tensor& dense) {
+  return reinterpret_cast<uintptr_t>(dense.data_ptr()) % 16 == 0 ? dense : dense.clone();
+}
+
 at::Tensor workspace(const at::Tensor& like, size_t bytes) {
   return at::empty({static_cast<int64_t>(bytes > 0 ? bytes : 1)}, like.options().dtype(at::kByte));
 }
@@ -112,13 +117,14 @@ at::Tensor spmm_csr_impl(const at::Tensor& rowptr, const at::Tensor& col, const 
 
   c10::DeviceGuard guard(dense.device());
   const at::Tensor rp = rowptr.contiguous(), cl = col.contiguous();
+  const at::Tensor dn = aligned(dense);
   const int64_t M = rowptr.size(0) - 1, D = dense.size(1);
   auto result = at::empty({M, D}, dense.options());
   spmm_csr_desc d{M, nnz1, dense.size(0), D, it, value_type_of(dense)};
   size_t ws_bytes = 0;
   raise_status(spmm_csr_workspace(&d, &ws_bytes), "spmm_csr");
   at::Tensor ws = workspace(dense, ws_bytes);
-  raise_status(spmm_csr_run(&d, rp.data_ptr(), cl.data_ptr(), value.data_ptr(), dense.data_ptr(),
+  raise_status(spmm_csr_run(&d, rp.data_ptr(), cl.data_ptr(), value.data_ptr(), dn.data_ptr(),
                             result.data_ptr(), ws.data_ptr(), ws_bytes, current_stream(dense)),
                "spmm_csr");
   return result;
@@ -137,6 +143,7 @@ at::Tensor run_mixed(const at::Tensor& Crowptr, const at::Tensor& Ccol_ids, cons
   c10::DeviceGuard guard(dense.device());
   const at::Tensor crp = Crowptr.contiguous(), ccl = Ccol_ids.contiguous();
   const at::Tensor vrp = Vrowptr.contiguous(), vcl = Vcol_ids.contiguous();
+  const at::Tensor dn = aligned(dense);
   spmm_mixed_desc d;
   d.block_windows = std::max<int64_t>(Crowptr.size(0) - 1, 0);
   d.block_count = Ccol_ids.size(0);
@@ -154,7 +161,7 @@ at::Tensor run_mixed(const at::Tensor& Crowptr, const at::Tensor& Ccol_ids, cons
   raise_status(spmm_mixed_workspace(&d, &ws_bytes), op_name);
   at::Tensor ws = workspace(dense, ws_bytes);
   raise_status(spmm_mixed_run(&d, crp.data_ptr(), ccl.data_ptr(), Cvalue.data_ptr(), vrp.data_ptr(),
-                              vcl.data_ptr(), Vvalue.data_ptr(), dense.data_ptr(), result.data_ptr(),
+                              vcl.data_ptr(), Vvalue.data_ptr(), dn.data_ptr(), result.data_ptr(),
                               ws.data_ptr(), ws_bytes, current_stream(dense)),
                op_name);
   return result;

@@ -85,7 +85,7 @@ def test_spmm_csr_fp16_width_1024(spmm_npu):
 def test_spmm_csr_long_rows_cross_ranges(spmm_npu, index_dtype):
     """Rows of 1000..5000 nonzeros cross many fixed ranges (fix-up path)."""
     rng = np.random.default_rng(11)
-    crow, col = random_csr(rng, 64, 6000, 5, long_rows=[(0, 1000), (5, 5000), (6, 129), (63, 2500)])
+    crow, col = random_csr(rng, 64, 6000, 5, long_rows=[(0, 1000), (5, 5000), (6, 257), (7, 513), (63, 2500)])
     vals = rng.uniform(-1, 1, col.size).astype(np.float32)
     B = rng.standard_normal((6000, 64)).astype(np.float32)
     out = run_csr(spmm_npu, crow, col, vals, B, index_dtype)

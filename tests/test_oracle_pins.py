@@ -1,0 +1,545 @@
+"""Pins of the CPU oracle (oracle/oracle.py + spmm_oracle.c) — CPU only.
+
+The reference repository holds no golden vectors and its Python/C++ extension
+cannot run here (it needs torch_npu and CANN), so each oracle function is
+pinned by checks that a plausible restatement mistake would fail:
+
+* the reference's own std-only headers, compiled from where they lie into
+  oracle/_ref/libref.so (bucket sort, column renumbering, packed transpose);
+* independent libraries (torch.sparse.mm, scipy.sparse, torch.searchsorted);
+* closed forms (per-window sorted distinct columns, tile grouping, P*A^T*P^T)
+  and exact reconstruction invariants;
+* hand-worked known answers derived from the reference's documented rules
+  (tie orders, the 295/505 cost model, the first-minimum rules);
+* brute-force optimality of the split points with exact rational arithmetic.
+"""
+
+import ctypes
+from fractions import Fraction
+
+import numpy as np
+import pytest
+import scipy.sparse as sp
+import torch
+
+import oracle as O
+
+
+def rand_csr(rng, rows, cols, max_deg, dup_free=True):
+    deg = rng.integers(0, max_deg + 1, size=rows)
+    parts = [np.sort(rng.choice(cols, min(int(d), cols), replace=False)) for d in deg]
+    crow = np.zeros(rows + 1, dtype=np.int64)
+    crow[1:] = np.cumsum([p.size for p in parts])
+    col = np.concatenate(parts).astype(np.int64) if parts else np.zeros(0, np.int64)
+    return crow, col
+
+
+def dense_of(crow, col, val, rows, cols):
+    d = np.zeros((rows, cols), dtype=np.float64)
+    for r in range(rows):
+        for p in range(crow[r], crow[r + 1]):
+            d[r, col[p]] = float(val[p])
+    return d
+
+
+# ------------------------------------------------------------------ SpMM
+
+def test_spmm_f64_matches_torch_and_scipy():
+    rng = np.random.default_rng(1)
+    crow, col = rand_csr(rng, 120, 90, 20)
+    val = rng.uniform(-1, 1, col.size)
+    B = rng.standard_normal((90, 33))
+    C = O.spmm_f64(crow, col, val, B)
+    ref_t = torch.sparse.mm(torch.sparse_csr_tensor(torch.from_numpy(crow), torch.from_numpy(col),
+                                                    torch.from_numpy(val), size=(120, 90)),
+                            torch.from_numpy(B)).numpy()
+    ref_s = sp.csr_matrix((val, col, crow), shape=(120, 90)) @ B
+    np.testing.assert_allclose(C, ref_t, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(C, ref_s, rtol=1e-12, atol=1e-12)
+
+
+def test_spmm_special_cases():
+    B = np.arange(12, dtype=np.float64).reshape(4, 3)
+    eye = np.arange(5, dtype=np.int64)
+    np.testing.assert_array_equal(O.spmm_f64(eye, eye[:4], np.ones(4), B), B)
+    np.testing.assert_array_equal(O.spmm_f64(np.zeros(3, np.int64), np.zeros(0, np.int64),
+                                             np.zeros(0), B), np.zeros((2, 3)))
+    # one nonzero per row: an exact scaled, permuted copy
+    out = O.spmm_f64(eye, np.array([3, 2, 1, 0]), np.array([2.0, -1.0, 0.5, 4.0]), B)
+    np.testing.assert_array_equal(out, np.stack([2 * B[3], -B[2], 0.5 * B[1], 4 * B[0]]))
+
+
+def test_cpu_reference_is_torch_sparse_fp32():
+    rng = np.random.default_rng(2)
+    crow, col = rand_csr(rng, 50, 40, 10)
+    val = rng.uniform(-1, 1, col.size).astype(np.float16)
+    B = rng.standard_normal((40, 16)).astype(np.float16)
+    out = O.cpu_reference(50, 40, crow, col, val, B)
+    assert out.dtype == torch.float32
+    np.testing.assert_allclose(out.numpy(), O.spmm_f64(crow, col, val, B), rtol=1e-5, atol=1e-5)
+
+
+# ------------------------------------------------------------- make_start
+
+def test_make_start_known_answers_and_searchsorted():
+    np.testing.assert_array_equal(O.make_start(np.array([0, 2, 4, 6]), 3), [0, 1, 2])
+    np.testing.assert_array_equal(O.make_start(np.array([0, 0, 0]), 4), [0, 0, 0, 0])
+    np.testing.assert_array_equal(O.make_start(np.array([0, 10]), 3), [0, 0, 0])
+    rng = np.random.default_rng(3)
+    for _ in range(20):
+        ptr = np.concatenate([[0], np.cumsum(rng.integers(0, 50, rng.integers(1, 300)))])
+        cores = int(rng.integers(1, 64))
+        total = int(ptr[-1])
+        if total <= 0:
+            expect = np.zeros(cores, np.int32)
+        else:
+            chunk = (total + cores - 1) // cores
+            tgt = torch.arange(cores, dtype=torch.int64) * chunk
+            expect = (torch.searchsorted(torch.from_numpy(ptr), tgt, right=True) - 1).clamp_min(0).numpy()
+        np.testing.assert_array_equal(O.make_start(ptr, cores), expect)
+
+
+# ---------------------------------------------- reference headers (_ref)
+
+def _ref():
+    lib = O.reference_library()
+    if lib is None:
+        pytest.skip("oracle/_ref/libref.so not built (reference checkout absent)")
+    return lib
+
+
+def _p64(a):
+    return a.ctypes.data_as(ctypes.POINTER(ctypes.c_int64))
+
+
+def test_bucket_sort_matches_reference_header():
+    lib = _ref()
+    rng = np.random.default_rng(4)
+    for trial in range(200):
+        n = int(rng.integers(0, 60))
+        ncols = 80
+        cols = rng.choice(ncols, n, replace=False).astype(np.int64)
+        occ = np.zeros(ncols, np.int64)
+        occ[cols] = rng.integers(1, 17, n)
+        if trial % 10 == 0 and n:
+            occ[cols[0]] = 17 if trial % 20 == 0 else 0  # error cases
+        mine_err = ref_rc = None
+        try:
+            mine = O.bucket_sort(cols, occ, 16)
+        except (ValueError, IndexError) as e:
+            mine_err = type(e)
+        ref = cols.copy()
+        ref_rc = lib.ref_bucket_sort(_p64(ref), ctypes.c_int64(n), _p64(occ), ctypes.c_int64(ncols),
+                                     ctypes.c_int64(16))
+        if ref_rc:
+            assert mine_err is {1: ValueError, 2: IndexError}[ref_rc]
+        else:
+            assert mine_err is None
+            np.testing.assert_array_equal(mine, ref)
+    # closed form: stable by (-occupancy, position)
+    cols = np.array([5, 2, 9, 1, 7], np.int64)
+    occ = np.zeros(10, np.int64)
+    occ[[5, 2, 9, 1, 7]] = [3, 16, 3, 1, 16]
+    np.testing.assert_array_equal(O.bucket_sort(cols, occ, 16), [2, 7, 5, 9, 1])
+
+
+@pytest.mark.parametrize("bits", [32, 64])
+def test_renumber_matches_reference_header(bits):
+    lib = _ref()
+    rng = np.random.default_rng(5 + bits)
+    dt = np.int32 if bits == 32 else np.int64
+    for trial in range(100):
+        ninv = int(rng.integers(1, 50))
+        inv = rng.permutation(ninv).astype(np.int64)
+        if trial % 7 == 0:
+            inv[rng.integers(0, ninv)] = -1
+        if trial % 11 == 0 and bits == 32:
+            inv[rng.integers(0, ninv)] = 2**31 + 5
+        cols = rng.integers(0, ninv + (trial % 5 == 0), size=int(rng.integers(0, 40))).astype(dt)
+        out = np.zeros(max(cols.size, 1), dt)
+        fn = lib.ref_renumber_i32 if bits == 32 else lib.ref_renumber_i64
+        ptr_t = ctypes.POINTER(ctypes.c_int32 if bits == 32 else ctypes.c_int64)
+        rc = fn(cols.ctypes.data_as(ptr_t), ctypes.c_int64(cols.size), _p64(inv),
+                ctypes.c_int64(ninv), out.ctypes.data_as(ptr_t))
+        try:
+            mine = O.renumber(cols, inv, dt)
+            assert rc == 0
+            np.testing.assert_array_equal(mine, out[: cols.size])
+        except (ValueError, IndexError, OverflowError) as e:
+            assert rc == {ValueError: 1, IndexError: 2, OverflowError: 3}[type(e)]
+
+
+def test_transpose_matches_reference_header_and_closed_form():
+    lib = _ref()
+    rng = np.random.default_rng(6)
+    for trial in range(60):
+        n = int(rng.integers(1, 70))
+        crow, col = rand_csr(rng, n, n, 8)
+        val = rng.standard_normal(col.size).astype(np.float32)
+        packed = n + int(rng.integers(0, 20))
+        inv = rng.permutation(packed)[:n].astype(np.int64)
+        rt, ct, vt = O.transpose(crow, col, val, inv, packed)
+        r_rt = np.zeros(packed + 1, np.int64)
+        r_ct = np.zeros(max(col.size, 1), np.int64)
+        r_vt = np.zeros(max(col.size, 1), np.uint32)
+        u32 = ctypes.POINTER(ctypes.c_uint32)
+        rc = lib.ref_transpose(_p64(crow), ctypes.c_int64(crow.size), _p64(col),
+                               val.view(np.uint32).ctypes.data_as(u32), ctypes.c_int64(col.size),
+                               _p64(inv), ctypes.c_int64(n), ctypes.c_int64(packed), _p64(r_rt),
+                               _p64(r_ct), r_vt.ctypes.data_as(u32))
+        assert rc == 0
+        np.testing.assert_array_equal(rt, r_rt)
+        np.testing.assert_array_equal(ct, r_ct[: col.size])
+        np.testing.assert_array_equal(vt.view(np.uint32), r_vt[: col.size])
+        # closed form: dense(T) = P A^T P^T
+        A = dense_of(crow, col, val, n, n)
+        P = np.zeros((packed, n))
+        P[inv, np.arange(n)] = 1
+        np.testing.assert_array_equal(dense_of(rt, ct, vt, packed, packed), P @ A.T @ P.T)
+    with pytest.raises(ValueError, match="does not end at nnz"):
+        O.transpose(np.array([0, 1, 3]), np.array([0, 1]), np.ones(2, np.float32),
+                    np.array([0, 1]), 2)
+
+
+# ------------------------------------------------------------- csr_to_bcsr
+
+def bcsr_closed_form(crow, col, val, nrows, W=16):
+    nwin = (nrows + W - 1) // W
+    cwp, uniq, value = [0], [], []
+    for w in range(nwin):
+        rows = range(w * W, min((w + 1) * W, nrows))
+        cols = sorted({int(col[p]) for r in rows for p in range(crow[r], crow[r + 1])})
+        slot = {c: len(uniq) + i for i, c in enumerate(cols)}
+        uniq += cols
+        blk = np.zeros((len(cols), 16), dtype=val.dtype)
+        for r in rows:
+            for p in range(crow[r], crow[r + 1]):
+                blk[slot[int(col[p])] - cwp[-1], r - w * W] = val[p]  # last write wins
+        value.append(blk.reshape(-1))
+        cwp.append(len(uniq))
+    return np.array(cwp), np.array(uniq, np.int64), (np.concatenate(value) if value else np.zeros(0, val.dtype))
+
+
+def test_csr_to_bcsr_known_answer():
+    # rows: 0 -> {1:a, 3:b}, 1 -> {0:c, 3:d}, 2 -> {4:e}; one padded window.
+    crow = np.array([0, 2, 4, 5], np.int64)
+    col = np.array([1, 3, 0, 3, 4], np.int64)
+    val = np.array([1, 2, 3, 4, 5], np.float32)
+    out = O.csr_to_bcsr(crow, col, val, 3, 5, 16)
+    np.testing.assert_array_equal(out["crow_window_ptr"], [0, 4])
+    np.testing.assert_array_equal(out["unique_col_ids"], [0, 1, 3, 4])
+    expect = np.zeros(64, np.float32)
+    expect[16 * 0 + 1] = 3
+    expect[16 * 1 + 0] = 1
+    expect[16 * 2 + 0] = 2
+    expect[16 * 2 + 1] = 4
+    expect[16 * 3 + 2] = 5
+    np.testing.assert_array_equal(out["value"], expect)
+    assert out["crow_window_ptr"].dtype == np.int64 and out["value"].dtype == np.float32
+
+
+@pytest.mark.parametrize("dt", [np.float16, np.float32])
+def test_csr_to_bcsr_closed_form_and_reconstruction(dt):
+    rng = np.random.default_rng(7)
+    for rows in (1, 15, 16, 17, 100):
+        crow, col = rand_csr(rng, rows, 60, 12)
+        val = rng.uniform(-1, 1, col.size).astype(dt)
+        out = O.csr_to_bcsr(crow.astype(np.int32), col.astype(np.int32), val, rows, 60, 16)
+        cwp, uniq, value = bcsr_closed_form(crow, col, val, rows)
+        np.testing.assert_array_equal(out["crow_window_ptr"], cwp)
+        np.testing.assert_array_equal(out["unique_col_ids"], uniq)
+        np.testing.assert_array_equal(out["value"].view(np.uint8), value.view(np.uint8))
+        assert out["unique_col_ids"].dtype == np.int32
+
+
+def test_csr_to_bcsr_duplicates_last_wins():
+    crow = np.array([0, 2, 3], np.int64)
+    col = np.array([3, 3, 3], np.int64)
+    val = np.array([1, 2, 7], np.float32)
+    out = O.csr_to_bcsr(crow, col, val, 2, 4, 16)
+    np.testing.assert_array_equal(out["unique_col_ids"], [3])
+    assert out["value"][0] == 2 and out["value"][1] == 7
+
+
+def test_csr_to_ascend_cube_known_answer_and_grouping():
+    crow = np.array([0, 2, 4, 5], np.int64)
+    col = np.array([1, 3, 0, 3, 4], np.int64)
+    val = np.array([1, 2, 3, 4, 5], np.float32)
+    out = O.csr_to_ascend_cube(crow, col, val, 3, 5, 16)
+    np.testing.assert_array_equal(out["crow_window_ptr"], [0, 1])
+    np.testing.assert_array_equal(out["unique_col_ids"], [0, 1, 3, 4] + [0] * 12)
+    expect = np.zeros(256, np.float32)
+    expect[16 * 1 + 0] = 3
+    expect[16 * 0 + 1] = 1
+    expect[16 * 0 + 2] = 2
+    expect[16 * 1 + 2] = 4
+    expect[16 * 2 + 3] = 5
+    np.testing.assert_array_equal(out["value"], expect)
+    # grouping form: cube tile (w, t) column c = BCSR block 16t + c of window w
+    rng = np.random.default_rng(8)
+    crow, col = rand_csr(rng, 70, 300, 60)
+    val = rng.uniform(-1, 1, col.size).astype(np.float32)
+    b = O.csr_to_bcsr(crow, col, val, 70, 300, 16)
+    c = O.csr_to_ascend_cube(crow, col, val, 70, 300, 16)
+    bw, cw = b["crow_window_ptr"], c["crow_window_ptr"]
+    for w in range(bw.size - 1):
+        nb = bw[w + 1] - bw[w]
+        assert cw[w + 1] - cw[w] == (nb + 15) // 16
+        for k in range(nb):
+            t, cc = cw[w] + k // 16, k % 16
+            assert c["unique_col_ids"][16 * t + cc] == b["unique_col_ids"][bw[w] + k]
+            tile = c["value"][256 * t: 256 * (t + 1)].reshape(16, 16)
+            np.testing.assert_array_equal(tile[:, cc], b["value"][16 * (bw[w] + k): 16 * (bw[w] + k + 1)])
+
+
+# ------------------------------------------------------- block_level_split
+
+def test_block_level_split_known_answer():
+    # window_size 2; blocks (w0,c0,2) (w0,c1,1) (w1,c2,2) (w1,c3,1); a = 1 -> k* = 2
+    crow = np.array([0, 2, 3, 4, 6], np.int64)
+    col = np.array([0, 1, 0, 2, 2, 3], np.int64)
+    val = np.array([10, 11, 20, 32, 42, 43], np.float32)
+    h = O.block_level_split(crow, col, val, 4, 4, 1.0, 2)
+    np.testing.assert_array_equal(h["crow_window_ptr"], [0, 1, 2])
+    np.testing.assert_array_equal(h["unique_col_ids"], [0, 2])
+    np.testing.assert_array_equal(h["value"], [10, 20, 32, 42])
+    np.testing.assert_array_equal(h["vrow_window_ptr"], [0, 1, 1, 1, 2])
+    np.testing.assert_array_equal(h["vcol_indices"], [1, 3])
+    np.testing.assert_array_equal(h["vvalue"], [11, 43])
+
+
+def _split_objective(counts_sorted, a):
+    """All |ratio - a| candidates as exact fractions (None for infinity)."""
+    nb = len(counts_sorted)
+    prefix = np.concatenate([[0], np.cumsum(counts_sorted)])
+    out = []
+    for k in range(nb + 1):
+        rem, nz = nb - k, int(prefix[k])
+        if nz == 0:
+            out.append(None if rem > 0 else abs(Fraction(0) - Fraction(a)))
+        else:
+            out.append(abs(Fraction(rem, nz) - Fraction(a)))
+    return out, prefix
+
+
+@pytest.mark.parametrize("a", [0.5842, (222 / 190) * 0.5, 0.1, 3.0, 295 / 505])
+def test_block_level_split_invariants_and_optimality(a):
+    rng = np.random.default_rng(int(a * 1000))
+    for rows in (5, 33, 130):
+        crow, col = rand_csr(rng, rows, 80, 14)
+        val = rng.uniform(-1, 1, col.size).astype(np.float32)
+        h = O.block_level_split(crow, col, val, rows, 80, a, 16)
+        A = dense_of(crow, col, val, rows, 80)
+        # reconstruction: BSR part + CSR part == A (original rows, padded to 16*nwin)
+        R = np.zeros(((rows + 15) // 16 * 16, 80))
+        cwp = h["crow_window_ptr"]
+        for w in range(cwp.size - 1):
+            for b in range(cwp[w], cwp[w + 1]):
+                R[16 * w:16 * w + 16, h["unique_col_ids"][b]] += h["value"][16 * b:16 * b + 16]
+            assert np.all(np.diff(h["unique_col_ids"][cwp[w]:cwp[w + 1]]) > 0)
+        vr = h["vrow_window_ptr"]
+        for r in range(vr.size - 1):
+            for p in range(vr[r], vr[r + 1]):
+                R[r, h["vcol_indices"][p]] += h["vvalue"][p]
+        np.testing.assert_array_equal(R[:rows], A)
+        assert not R[rows:].any()
+        # every block lies wholly in one part; moved blocks are the least dense
+        occ = {}
+        for w in range((rows + 15) // 16):
+            for r in range(16 * w, min(16 * w + 16, rows)):
+                for p in range(crow[r], crow[r + 1]):
+                    occ[(w, int(col[p]))] = occ.get((w, int(col[p])), 0) + 1
+        moved = {(r // 16, int(h["vcol_indices"][p])) for r in range(vr.size - 1)
+                 for p in range(vr[r], vr[r + 1])}
+        kept = set(occ) - moved
+        if moved and kept:
+            assert max(occ[b] for b in moved) <= min(occ[b] for b in kept)
+        # k* = number of moved blocks is the first minimiser (in double) of |ratio - a|
+        counts = sorted(occ.values())
+        k_star = len(moved)
+        cands, prefix = _split_objective(counts, a)
+        assert int(prefix[k_star]) == h["vcol_indices"].size
+        best = min((c for c in cands if c is not None), default=None)
+        if best is not None and cands[k_star] is not None:
+            assert float(cands[k_star]) <= float(best) * (1 + 1e-12) + 1e-15
+            for k in range(k_star):
+                assert cands[k] is None or float(cands[k]) > float(cands[k_star]) * (1 - 1e-12) - 1e-15
+
+
+# -------------------------------------------------------------- preprocess
+
+def _hand_matrix():
+    """Window 0: all 16 rows hold columns {0, 1}; window 1: row 16+i holds column 16+i."""
+    rows = []
+    for r in range(16):
+        rows.append([0, 1])
+    for r in range(16, 32):
+        rows.append([r])
+    crow = np.concatenate([[0], np.cumsum([len(x) for x in rows])]).astype(np.int64)
+    col = np.concatenate(rows).astype(np.int64)
+    val = (np.arange(col.size) + 1).astype(np.float32)
+    return crow, col, val
+
+
+def test_preprocess_known_answer():
+    crow, col, val = _hand_matrix()
+    p = O.preprocess(crow, col, val, 32, 32, 16, False)
+    # densities 16 and 1; pos 0: 2/295 < 16/505; pos 1: 18/295 >= 0/505 -> marginal = window 1
+    assert p["marginal_window"][0] == 1 and p["marginal_total_blocks"][0] == 16
+    # max((2+q)/295, (16-q)/505) is smallest at q = 5
+    assert p["marginal_aic_blocks"][0] == 5 and p["shared_windows"][0] == 1
+    assert p["estimated_aic_cost"][0] == 7 / 295 and p["estimated_aiv_cost"][0] == 11 / 505
+    assert p["estimated_max_cost"][0] == 7 / 295
+    np.testing.assert_array_equal(p["crow_window_ptr"], [0, 2, 7])
+    np.testing.assert_array_equal(p["unique_col_ids"], [0, 1, 16, 17, 18, 19, 20])
+    np.testing.assert_array_equal(p["permutation"], np.arange(32))
+    np.testing.assert_array_equal(p["inv_permutation"], np.arange(32))
+    assert p["packed_rows"][0] == 32 and p["packed_layout_supported"][0] == 0
+    np.testing.assert_array_equal(p["vrow_window_ptr"], [0] * 22 + list(range(1, 12)))
+    np.testing.assert_array_equal(p["vcol_indices"], np.arange(21, 32))
+    # block 2 (column 16) of slot 1 holds row 16's value at row offset 0
+    v = p["value"].reshape(-1, 16)
+    assert v[2, 0] == val[32] and v[2, 1:].sum() == 0
+    np.testing.assert_array_equal(v[0], val[0:32:2])
+    for key in ("renumbered_unique_col_ids", "transpose_crow_window_ptr", "transpose_vvalue"):
+        assert p[key].size == 0
+
+
+def test_preprocess_density_tie_orders_by_window_id():
+    # three windows of equal density 1 (one nonzero per row, distinct columns)
+    crow = np.arange(49, dtype=np.int64)
+    col = np.arange(48, dtype=np.int64)
+    val = np.ones(48, np.float32)
+    p = O.preprocess(crow, col, val, 48, 48, 16, False)
+    # pos 0: 16/295 >= 32/505 is False; pos 1: 32/295 >= 16/505 -> marginal = window 1
+    assert p["marginal_window"][0] == 1
+    # q*: max((16+q)/295, (32-q)/505) -> q = 1 ((17/295=.0576, 31/505=.0614) vs q=2 ...)
+    costs = [max((16 + q) / 295, (32 - q) / 505) for q in range(17)]
+    assert p["marginal_aic_blocks"][0] == int(np.argmin(costs))
+    # window 0 is the first AIC slot, window 2 follows in the AIV rows
+    assert list(p["permutation"][:16]) == list(range(16))
+
+
+def _check_preprocess_invariants(crow, col, val, rows, cols, p, graph_layout):
+    nnz = col.size
+    aic_nnz = int(np.count_nonzero(p["value"]))
+    assert aic_nnz + p["vcol_indices"].size == nnz  # nnz conservation (values nonzero)
+    perm, inv = p["permutation"], p["inv_permutation"]
+    packed = int(p["packed_rows"][0])
+    assert perm.size == packed and inv.size == rows
+    real = perm[perm >= 0]
+    assert sorted(real.tolist()) == list(range(rows))
+    assert np.all(perm[inv] == np.arange(rows))
+    # reconstruction of P*A (packed rows) from the block and vector parts
+    A = dense_of(crow, col, val, rows, cols)
+    R = np.zeros((max(packed, 16 * (p["crow_window_ptr"].size - 1)), cols))
+    cwp = p["crow_window_ptr"]
+    for s in range(cwp.size - 1):
+        ids = p["unique_col_ids"][cwp[s]:cwp[s + 1]]
+        assert np.all(np.diff(ids) > 0)
+        for b in range(cwp[s], cwp[s + 1]):
+            R[16 * s:16 * s + 16, p["unique_col_ids"][b]] += p["value"][16 * b:16 * b + 16]
+    vr = p["vrow_window_ptr"]
+    assert vr.size == packed + 1
+    for r in range(packed):
+        for q in range(vr[r], vr[r + 1]):
+            R[r, p["vcol_indices"][q]] += p["vvalue"][q]
+    PA = np.zeros_like(R)
+    PA[inv] = A
+    np.testing.assert_array_equal(R, PA)
+    if graph_layout and rows == cols:
+        np.testing.assert_array_equal(p["renumbered_unique_col_ids"], inv[p["unique_col_ids"]])
+        np.testing.assert_array_equal(p["renumbered_vcol_indices"], inv[p["vcol_indices"]])
+        # transpose_* reassembles P*A^T*P^T
+        T = np.zeros((packed, packed))
+        tw = p["transpose_crow_window_ptr"]
+        for s in range(tw.size - 1):
+            for b in range(tw[s], tw[s + 1]):
+                T[16 * s:16 * s + 16, p["transpose_unique_col_ids"][b]] += p["transpose_value"][16 * b:16 * b + 16]
+        tv = p["transpose_vrow_window_ptr"]
+        for r in range(tv.size - 1):
+            for q in range(tv[r], tv[r + 1]):
+                T[r, p["transpose_vcol_indices"][q]] += p["transpose_vvalue"][q]
+        P = np.zeros((packed, rows))
+        P[inv, np.arange(rows)] = 1
+        np.testing.assert_array_equal(T, P @ A.T @ P.T)
+
+
+@pytest.mark.parametrize("graph_layout", [False, True])
+def test_preprocess_invariants_random(graph_layout):
+    rng = np.random.default_rng(9)
+    for rows, maxd in ((40, 12), (100, 30), (257, 6)):
+        crow, col = rand_csr(rng, rows, rows, maxd)
+        # a few dense windows so the split is non-trivial
+        val = rng.uniform(0.5, 1, col.size).astype(np.float32)
+        p = O.preprocess(crow, col, val, rows, rows, 16, graph_layout)
+        _check_preprocess_invariants(crow, col, val, rows, rows, p, graph_layout)
+
+
+def test_preprocess_marginal_split_is_first_minimum():
+    """q* and the recorded costs follow the brute-force first minimum of
+    max(aic, aiv) over every prefix of the occupancy-sorted marginal blocks."""
+    rng = np.random.default_rng(10)
+    for _ in range(25):
+        rows = int(rng.integers(17, 120))
+        crow, col = rand_csr(rng, rows, rows, int(rng.integers(2, 20)))
+        val = np.ones(col.size, np.float32)
+        p = O.preprocess(crow, col, val, rows, rows, 16, False)
+        w = int(p["marginal_window"][0])
+        if w < 0:
+            continue
+        # window stats and the prefix before the marginal window
+        nwin = (rows + 15) // 16
+        stats = []
+        for ww in range(nwin):
+            rr = range(16 * ww, min(16 * ww + 16, rows))
+            cs = [int(col[q]) for r in rr for q in range(crow[r], crow[r + 1])]
+            nb = len(set(cs))
+            stats.append((-(len(cs) / nb if nb else 0.0), ww, len(cs), nb))
+        stats.sort()
+        pos = [s[1] for s in stats].index(w)
+        prefix = sum(s[3] for s in stats[:pos])
+        remaining = col.size - sum(s[2] for s in stats[:pos])
+        rr = range(16 * w, min(16 * w + 16, rows))
+        first_seen, occ = [], {}
+        for r in rr:
+            for q in range(crow[r], crow[r + 1]):
+                c = int(col[q])
+                if c not in occ:
+                    first_seen.append(c)
+                occ[c] = occ.get(c, 0) + 1
+        order = sorted(first_seen, key=lambda c: (-occ[c], first_seen.index(c)))
+        costs, assigned = [], 0
+        for q in range(len(order) + 1):
+            costs.append(max(Fraction(prefix + q, 295), Fraction(remaining - assigned, 505)))
+            if q < len(order):
+                assigned += occ[order[q]]
+        q_star = int(p["marginal_aic_blocks"][0])
+        assert costs[q_star] == min(costs) or float(costs[q_star]) == float(min(costs))
+        assert all(float(costs[q]) > float(costs[q_star]) for q in range(q_star))
+
+
+def test_preprocess_errors():
+    crow = np.array([0, 1], np.int64)
+    with pytest.raises(RuntimeError, match="16-row window"):
+        O.preprocess(crow, np.array([0]), np.ones(1, np.float32), 1, 1, 8, False)
+    with pytest.raises(RuntimeError, match="column index out of range"):
+        O.preprocess(crow, np.array([5]), np.ones(1, np.float32), 1, 3, 16, False)
+    # duplicate coordinates in the marginal window: occupancy > 16 is rejected
+    crow = np.array([0] + [17] + [17] * 15, np.int64)
+    with pytest.raises(ValueError, match="coalesce duplicate CSR entries"):
+        O.preprocess(crow, np.zeros(17, np.int64), np.ones(17, np.float32), 16, 4, 16, False)
+
+
+# ---------------------------------------------------------- pack / restore
+
+def test_pack_restore_closed_form():
+    rng = np.random.default_rng(12)
+    x = rng.standard_normal((20, 5))
+    inv = rng.permutation(32)[:20]
+    packed = O.pack_node_tensor(x, inv, 32)
+    assert packed.shape == (32, 5)
+    np.testing.assert_array_equal(packed[inv], x)
+    assert not packed[np.setdiff1d(np.arange(32), inv)].any()
+    np.testing.assert_array_equal(O.restore_node_tensor(packed, inv), x)
+    assert O.pack_node_tensor(x, inv).shape[0] == inv.max() + 1
