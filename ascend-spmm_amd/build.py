@@ -30,11 +30,12 @@ HIP_SOURCES = [
     "spmm_gather.hip",
     "spmm_block.hip",
     "permute_rows.hip",
+    "preprocess.hip",
 ]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
-# Packed-FP32 instructions are disabled for all device code (see the
-# repository's design notes on gfx950 code generation).
+# Packed-FP32 instructions (v_pk_*_f32) are disabled for all device code:
+# some of their forms have produced silently wrong results on MI355X boxes.
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",
     "-O3",

@@ -20,7 +20,11 @@ if _HERE not in sys.path:
     sys.path.insert(0, _HERE)
 
 from custom_ops_lib import (  # noqa: E402
+    block_level_split,
+    csr_to_ascend_cube,
+    csr_to_bcsr,
     pack_rows as _pack_rows,
+    preprocess,
     restore_rows as _restore_rows,
     spmm_ascend_cube,
     spmm_ascend_cube_aic_without_pipeline,
@@ -74,7 +78,11 @@ def restore_node_tensor(packed_tensor, inv_permutation):
 
 
 __all__ = [
+    "block_level_split",
+    "csr_to_ascend_cube",
+    "csr_to_bcsr",
     "pack_node_tensor",
+    "preprocess",
     "restore_node_tensor",
     "spmm_ascend_cube",
     "spmm_ascend_cube_aic_without_pipeline",

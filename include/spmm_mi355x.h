@@ -161,6 +161,126 @@ spmm_status spmm_restore_rows(const void* packed, int64_t packed_rows, int64_t r
                               const int64_t* inv, int64_t rows, void* dst,
                               spmm_stream stream);
 
+/* ------------------------------------------------------------------------
+ * Preprocessing on the GPU (layout conversion and work partitioning).
+ *
+ * The reference runs these on the host with ATen accessors; here they are
+ * device pipelines whose outputs are bit-identical to the reference's
+ * (integer arrays, and values copied bit for bit).  Index outputs use the
+ * input's index type; permutations are int64.
+ *
+ * Each conversion is two calls on the same workspace:
+ *   *_workspace(...)  bytes of workspace (depends only on the sizes)
+ *   *_plan(...)       runs the pipeline into the workspace and returns the
+ *                     output sizes (synchronises the stream)
+ *   *_fill(...)       writes the outputs into caller buffers of those sizes
+ * Input requirements (checked on the device, reported by *_plan):
+ *   row pointer monotone within [0, nnz]  -> SPMM_ERR_INVALID_ARGUMENT
+ *   column ids in [0, cols)               -> SPMM_ERR_CONTRACT
+ *   (bcsr / cube) ascending columns per row, as the reference's docs
+ *   require (extension/custom_op.cpp:1430,1440) -> SPMM_ERR_INVALID_ARGUMENT
+ * ---------------------------------------------------------------------- */
+typedef struct spmm_csr_matrix {
+  int64_t rows;        /* rowptr holds rows + 1 entries                    */
+  int64_t cols;
+  int64_t nnz;         /* extent of col[] and value[]                      */
+  int32_t index_type;  /* spmm_index_type                                  */
+  int32_t value_type;  /* spmm_value_type: F16, F32 or F64 (copied only)   */
+  const void* rowptr;  /* device pointers                                  */
+  const void* col;
+  const void* value;
+} spmm_csr_matrix;
+
+/* csr_to_bcsr: BCSR(16x1).  Replaces ToBCSR / csr_to_bcsr
+ * (extension/custom_op.cpp:594-746).  Outputs: crow_window_ptr[nwin+1],
+ * unique_col_ids[blocks], value[16*blocks], nwin = ceil(rows/window_size),
+ * 1 <= window_size <= 16. */
+size_t spmm_bcsr_workspace(const spmm_csr_matrix* m, int64_t window_size);
+spmm_status spmm_bcsr_plan(const spmm_csr_matrix* m, int64_t window_size, void* workspace,
+                           size_t workspace_bytes, spmm_stream stream, int64_t* blocks);
+spmm_status spmm_bcsr_fill(const spmm_csr_matrix* m, int64_t window_size, void* workspace,
+                           size_t workspace_bytes, void* crow_window_ptr, void* unique_col_ids,
+                           void* value, spmm_stream stream);
+
+/* csr_to_ascend_cube: 16x16 cube tiles.  Replaces your_logic_kernel /
+ * csr_to_ascend_cube (extension/custom_op.cpp:429-592).  Outputs:
+ * crow_window_ptr[nwin+1] (tile offsets), unique_col_ids[16*tiles] (zero
+ * padded per window), value[256*tiles]. */
+size_t spmm_cube_workspace(const spmm_csr_matrix* m, int64_t window_size);
+spmm_status spmm_cube_plan(const spmm_csr_matrix* m, int64_t window_size, void* workspace,
+                           size_t workspace_bytes, spmm_stream stream, int64_t* tiles);
+spmm_status spmm_cube_fill(const spmm_csr_matrix* m, int64_t window_size, void* workspace,
+                           size_t workspace_bytes, void* crow_window_ptr, void* unique_col_ids,
+                           void* value, spmm_stream stream);
+
+/* block_level_split: density-threshold BCSR(window_size x 1) + CSR split.
+ * Replaces hybrid_split_impl / block_level_split
+ * (extension/custom_op.cpp:1139-1348, 1390-1412).  Outputs:
+ * crow_window_ptr[nwin+1], unique_col_ids[kept_blocks],
+ * value[window_size*kept_blocks], vrow_window_ptr[window_size*nwin+1],
+ * vcol_indices[vector_nnz], vvalue[vector_nnz]. */
+size_t spmm_hybrid_workspace(const spmm_csr_matrix* m, int64_t window_size);
+spmm_status spmm_hybrid_plan(const spmm_csr_matrix* m, double a, int64_t window_size,
+                             void* workspace, size_t workspace_bytes, spmm_stream stream,
+                             int64_t* kept_blocks, int64_t* vector_nnz);
+spmm_status spmm_hybrid_fill(const spmm_csr_matrix* m, double a, int64_t window_size,
+                             void* workspace, size_t workspace_bytes, void* crow_window_ptr,
+                             void* unique_col_ids, void* value, void* vrow_window_ptr,
+                             void* vcol_indices, void* vvalue, spmm_stream stream);
+
+/* preprocess: the 295/505 cost-model AIC/AIV task mapping with the marginal
+ * window split, row permutation and (graph_layout on a square matrix) the
+ * renumbered columns and the fixed-layout transpose P*A^T*P^T.  Replaces
+ * taskmapping / preprocess (extension/custom_op.cpp:749-1137, with
+ * boundary_bucket_sort.h and packed_column_reindex.h).  window_size must be
+ * 16 (SPMM_ERR_CONTRACT otherwise, as the reference's TORCH_CHECK). */
+typedef struct spmm_taskmap_info {
+  int64_t aic_windows;            /* crow_window_ptr: aic_windows + 1       */
+  int64_t aic_blocks;             /* unique_col_ids; value: 16*aic_blocks   */
+  int64_t packed_rows;            /* vrow_window_ptr: packed_rows + 1; permutation */
+  int64_t vector_nnz;             /* vcol_indices, vvalue                   */
+  int64_t packed_layout_supported;
+  int64_t marginal_window;        /* -1 if none                             */
+  int64_t marginal_aic_blocks;
+  int64_t marginal_total_blocks;
+  int64_t shared_windows;
+  double estimated_aic_cost;
+  double estimated_aiv_cost;
+  double estimated_max_cost;
+  /* transpose_* (graph layout only; all 0 otherwise)                     */
+  int64_t t_windows;              /* transpose_crow_window_ptr: t_windows+1 */
+  int64_t t_blocks;               /* transpose_unique_col_ids; value 16*t_blocks */
+  int64_t t_rows;                 /* transpose_vrow_window_ptr: t_rows + 1  */
+  int64_t t_vector_nnz;
+} spmm_taskmap_info;
+
+typedef struct spmm_taskmap_out {
+  void* crow_window_ptr;
+  void* unique_col_ids;
+  void* value;
+  void* vrow_window_ptr;
+  void* vcol_indices;
+  void* vvalue;
+  void* renumbered_unique_col_ids;  /* graph layout: aic_blocks entries   */
+  void* renumbered_vcol_indices;    /* graph layout: vector_nnz entries   */
+  void* transpose_crow_window_ptr;
+  void* transpose_unique_col_ids;
+  void* transpose_value;
+  void* transpose_vrow_window_ptr;
+  void* transpose_vcol_indices;
+  void* transpose_vvalue;
+  int64_t* permutation;             /* packed_rows entries (-1 = padding)  */
+  int64_t* inv_permutation;         /* rows entries                        */
+} spmm_taskmap_out;
+
+size_t spmm_taskmap_workspace(const spmm_csr_matrix* m, int64_t window_size, int graph_layout);
+spmm_status spmm_taskmap_plan(const spmm_csr_matrix* m, int64_t window_size, int graph_layout,
+                              void* workspace, size_t workspace_bytes, spmm_stream stream,
+                              spmm_taskmap_info* info);
+spmm_status spmm_taskmap_fill(const spmm_csr_matrix* m, int64_t window_size, int graph_layout,
+                              void* workspace, size_t workspace_bytes,
+                              const spmm_taskmap_out* out, spmm_stream stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif
