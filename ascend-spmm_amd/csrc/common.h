@@ -47,26 +47,41 @@ inline int64_t gather_slot_floats(int64_t width) { return (width + 63) / 64 * 64
 // ---- internal launchers (defined in the .hip files) ----------------------
 
 // Vector (CSR gather) part over rows [row_lo, row_hi) of the CSR given by
-// (rowptr, col, value) with `nnz` valid entries.  Writes rows to `out`.
+// (rowptr, col, value): rowptr holds vrows + 1 entries (rows >= vrows are
+// empty) and col/value hold `nnz`.  Writes every row of [row_lo, row_hi).
+// With a block part (Crowptr != nullptr, cwin windows, climit usable blocks),
+// the vector sums of rows in block windows with blocks go to `vpart` (fp32)
+// instead of `out`, and their empty rows are left to the block kernel.
 spmm_status launch_gather(int32_t index_type, int32_t value_type,
                           const void* rowptr, const void* col, const void* value,
-                          int64_t nnz, int64_t row_lo, int64_t row_hi,
+                          int64_t nnz, int64_t vrows, int64_t row_lo, int64_t row_hi,
                           const void* dense, int64_t dense_rows, int64_t width,
                           void* out, void* workspace, size_t workspace_bytes,
+                          const void* Crowptr, int64_t cwin, int64_t climit, float* vpart,
                           hipStream_t stream);
 
 // Workspace bytes launch_gather may use for at most `nnz` vector nonzeros.
 size_t gather_workspace_bytes(int64_t nnz, int64_t width);
 
-// Block (BCSR 16x1) part: every window s < windows computes its block sum on
-// MFMA, adds the vector-part nonzeros of rows 16*s .. 16*s+15 that exist
-// (row < vector_rows), and writes rows 16*s .. 16*s+15 of `out`.
+// Blocks of a window handled by one work-group before the window is split
+// (fixed per value type, so results do not depend on the width).
+template <typename T>
+constexpr int64_t block_chunk() { return sizeof(T) == 2 ? 512 : 256; }
+inline int64_t block_chunk_for(int32_t value_type) { return value_type == SPMM_VALUE_F16 ? 512 : 256; }
+
+// Number of fixed overflow ranges for `blocks` usable blocks.
+int64_t block_overflow_ranges(int64_t blocks, int64_t kbig);
+
+// Block (BCSR 16x1) part.  Runs after the gather pass: every window with
+// blocks is written to `out` as block sum + the fp32 vector sums the gather
+// pass left in `vpart` ([16*windows][width]) for its rows with vector
+// nonzeros, rounded once.  `slots` holds the pieces of windows longer than
+// block_chunk ([ranges][2][16][width] fp32).
 spmm_status launch_block(int32_t index_type, int32_t value_type,
                          const void* Crowptr, const void* Ccol, const void* Cvalue,
                          int64_t windows, int64_t block_count, int64_t block_values,
-                         const void* Vrowptr, const void* Vcol, const void* Vvalue,
-                         int64_t vector_rows, int64_t vector_nnz,
+                         const void* Vrowptr, int64_t vector_rows, int64_t vector_nnz,
                          const void* dense, int64_t dense_rows, int64_t width,
-                         void* out, hipStream_t stream);
+                         void* out, const float* vpart, float* slots, hipStream_t stream);
 
 }  // namespace spmm

@@ -21,21 +21,26 @@
 //  * Waves of the work-group take 64-column groups round-robin; each group
 //    runs the whole K loop, so every output element sees the same MFMA
 //    sequence for every width N.
-//  * The fp32 window tile goes to LDS; the work-group then adds the vector
-//    (CSR) nonzeros of the window's rows in order (shared-window residuals of
-//    preprocess and the CSR part of block_level_split), rounds once and
-//    stores coalesced rows.
+//  * Windows longer than a fixed chunk (block_chunk: 512 blocks fp16, 256
+//    fp32) are cut at fixed block positions: the window's own work-group
+//    takes its first chunk, and "overflow" work-groups take the rest in fixed
+//    global block ranges (only one window can overflow into a range).  A
+//    combine kernel adds the pieces in order, so the split is deterministic.
+//  * Vector (CSR) nonzeros of rows inside block windows are summed by the CSR
+//    gather kernel first (so long rows get its load balance) and left in an
+//    fp32 workspace; the block kernel adds them after the block sum and
+//    rounds once.
 //  * blockIdx -> window is XCD-aware: consecutive windows land on the same XCD
 //    (work-groups are dealt round-robin over the 8 XCDs), so neighbouring
 //    windows that gather the same dense rows share that XCD's L2.
 #include "common.h"
 #include "lanevec.h"
+#include "wgsearch.h"
 
 namespace spmm {
 namespace {
 
 using lanes::LaneVec;
-using lanes::accumulate;
 using lanes::clampi;
 
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
@@ -127,81 +132,201 @@ __device__ inline void window_group_f32(float* __restrict__ tile, const I* __res
   }
 }
 
+// Arguments shared by the block kernels.
 template <typename T, typename I>
-__global__ __launch_bounds__(256) void block_windows(
-    const I* __restrict__ Crowptr, const I* __restrict__ Ccol, const T* __restrict__ Cvalue,
-    int64_t windows, int64_t block_limit, const I* __restrict__ Vrowptr,
-    const I* __restrict__ Vcol, const T* __restrict__ Vvalue, int64_t vector_rows,
-    int64_t vector_nnz, const T* __restrict__ dense, int64_t K, int64_t N, T* __restrict__ out,
-    int64_t per_xcd) {
-  extern __shared__ float tile[];  // [16][N] fp32
-  const int64_t s = static_cast<int64_t>(blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
-  if (s >= windows) return;  // uniform over the work-group
+struct BlockArgs {
+  const I* Crowptr;
+  const I* Ccol;
+  const T* Cvalue;
+  int64_t windows, limit;  // block windows; usable blocks = min(Ccol, Cvalue/16)
+  const I* Vrowptr;
+  int64_t vrows, vnnz;     // vector part: rows and nonzeros
+  const T* dense;
+  int64_t K, N;
+  T* out;
+  const float* vpart;      // [16*windows][N] fp32 vector sums of block-window rows (gather pass)
+  float* slots;            // [noverflow][2][16][N] fp32 partials of windows longer than kbig
+  int64_t kbig, noverflow, per_xcd;
 
-  const int64_t b0 = clampi(static_cast<int64_t>(Crowptr[s]), 0, block_limit);
-  const int64_t b1 = clampi(static_cast<int64_t>(Crowptr[s + 1]), b0, block_limit);
+  __device__ inline int64_t crp(int64_t s) const { return clampi(static_cast<int64_t>(Crowptr[s]), 0, limit); }
+  __device__ inline int64_t vrp(int64_t r) const {
+    return clampi(static_cast<int64_t>(Vrowptr[r < vrows ? r : vrows]), 0, vnnz);
+  }
+  // Row r has vector-part nonzeros (then the gather pass left their sum in vpart).
+  __device__ inline bool row_has_vector(int64_t r) const { return r < vrows && vrp(r) != vrp(r + 1); }
+};
+
+// Fills the LDS tile with the MFMA sum of blocks [b0, b1) of window s.
+template <typename T, typename I>
+__device__ inline void window_tile(const BlockArgs<T, I>& a, float* tile, int64_t b0, int64_t b1) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int waves = blockDim.x >> 6;
-  const int64_t groups = (N + 63) / 64;
+  const int64_t groups = (a.N + 63) / 64;
   for (int64_t g = wave; g < groups; g += waves) {
     if constexpr (sizeof(T) == 2)
-      window_group_f16<I>(tile, Ccol, Cvalue, b0, b1, dense, K, N, 64 * g, lane);
+      window_group_f16<I>(tile, a.Ccol, a.Cvalue, b0, b1, a.dense, a.K, a.N, 64 * g, lane);
     else
-      window_group_f32<I>(tile, Ccol, Cvalue, b0, b1, dense, K, N, 64 * g, lane);
-  }
-  __syncthreads();
-
-  constexpr int V = LaneVec<T>::V;
-  const int64_t chunks = N / V;
-  for (int64_t it = threadIdx.x; it < 16 * chunks; it += blockDim.x) {
-    const int64_t r = it / chunks;
-    const int64_t c0 = (it - r * chunks) * V;
-    float acc[V];
-#pragma unroll
-    for (int i = 0; i < V; ++i) acc[i] = tile[r * N + c0 + i];
-    const int64_t row = 16 * s + r;
-    if (row < vector_rows) {
-      const int64_t a = clampi(static_cast<int64_t>(Vrowptr[row]), 0, vector_nnz);
-      const int64_t b = clampi(static_cast<int64_t>(Vrowptr[row + 1]), 0, vector_nnz);
-      accumulate<T, I>(acc, a, b, Vcol, Vvalue, dense, K, N, c0);
-    }
-    LaneVec<T>::store(out + row * N + c0, acc);
+      window_group_f32<I>(tile, a.Ccol, a.Cvalue, b0, b1, a.dense, a.K, a.N, 64 * g, lane);
   }
 }
 
+// Finishes window s from its fp32 block sum (LDS tile or `src`): adds the
+// vector sums of rows that have them (block first, then vector part), rounds
+// once and writes rows 16*s .. 16*s+15.
 template <typename T, typename I>
-spmm_status block_typed(const void* Crowptr, const void* Ccol, const void* Cvalue,
-                        int64_t windows, int64_t block_count, int64_t block_values,
-                        const void* Vrowptr, const void* Vcol, const void* Vvalue,
+__device__ inline void finish_window(const BlockArgs<T, I>& a, int64_t s, const float* src) {
+  constexpr int V = LaneVec<T>::V;
+  __shared__ unsigned s_vec;  // bit r: row 16*s + r has vector nonzeros
+  if (threadIdx.x == 0) s_vec = 0;
+  __syncthreads();
+  if (threadIdx.x < 16 && a.row_has_vector(16 * s + threadIdx.x)) atomicOr(&s_vec, 1u << threadIdx.x);
+  __syncthreads();
+  const unsigned vec = s_vec;
+  const int64_t chunks = a.N / V;
+  for (int64_t it = threadIdx.x; it < 16 * chunks; it += blockDim.x) {
+    const int64_t r = it / chunks;
+    const int64_t c0 = (it - r * chunks) * V;
+    const int64_t row = 16 * s + r;
+    float acc[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[i] = src[r * a.N + c0 + i];
+    if (vec >> r & 1u) {
+      const float* vp = a.vpart + row * a.N + c0;
+#pragma unroll
+      for (int i = 0; i < V; ++i) acc[i] = acc[i] + vp[i];
+    }
+    LaneVec<T>::store(a.out + row * a.N + c0, acc);
+  }
+}
+
+// Copies the 16 x N fp32 tile to a workspace slot.
+__device__ inline void save_tile(const float* tile, int64_t N, float* dst) {
+  for (int64_t i = threadIdx.x; i < 16 * N; i += blockDim.x) dst[i] = tile[i];
+}
+
+// Work-groups [0, 8*per_xcd): window s (XCD-aware order) computes its first
+// kbig blocks; a window with at most kbig blocks is finished here.  A longer
+// window leaves its first-chunk sum in slot (k0, 1), k0 = (b0 + kbig) / kbig.
+// Work-groups 8*per_xcd + k: overflow range k = blocks [k*kbig, (k+1)*kbig).
+// Only the window holding block k*kbig can have blocks past its first chunk
+// in that range; that segment's sum goes to slot (k, 0).
+template <typename T, typename I>
+__global__ __launch_bounds__(256) void block_windows(BlockArgs<T, I> a) {
+  extern __shared__ float tile[];  // [16][N] fp32
+  const int64_t lead = a.per_xcd * kXcds;
+  const int64_t g = blockIdx.x;
+  if (g < lead) {
+    const int64_t s = (g % kXcds) * a.per_xcd + g / kXcds;
+    if (s >= a.windows) return;  // uniform over the work-group
+    const int64_t b0 = a.crp(s);
+    int64_t b1 = a.crp(s + 1);
+    if (b1 <= b0) return;  // empty window: rows handled by the vector pass
+    const bool single = b1 - b0 <= a.kbig;
+    if (!single) b1 = b0 + a.kbig;
+    window_tile(a, tile, b0, b1);
+    __syncthreads();
+    if (single)
+      finish_window(a, s, tile);
+    else
+      save_tile(tile, a.N, a.slots + (2 * ((b0 + a.kbig) / a.kbig) + 1) * 16 * a.N);
+    return;
+  }
+  const int64_t k = g - lead;
+  if (k >= a.noverflow) return;
+  const int64_t bk = k * a.kbig;
+  // s = window holding block bk: last s with crp(s) <= bk.
+  int64_t first_above, unused;
+  wg_lower_bound2([&](int64_t i) { return a.crp(i); }, 0, a.windows, bk + 1, bk + 1, first_above, unused);
+  const int64_t s = first_above - 1;
+  if (s < 0 || s >= a.windows) return;
+  const int64_t b0 = a.crp(s), b1 = a.crp(s + 1);
+  if (!(b0 < bk && b1 > b0 + a.kbig)) return;
+  const int64_t lo = b0 + a.kbig > bk ? b0 + a.kbig : bk;
+  const int64_t hi = b1 < bk + a.kbig ? b1 : bk + a.kbig;
+  if (lo >= hi) return;
+  window_tile(a, tile, lo, hi);
+  __syncthreads();
+  save_tile(tile, a.N, a.slots + (2 * k) * 16 * a.N);
+}
+
+// Work-group k: if a window's blocks past its first chunk start in overflow
+// range k, add first chunk + segments k, k+1, ... in order (into LDS) and
+// finish the window.
+template <typename T, typename I>
+__global__ __launch_bounds__(256) void block_combine(BlockArgs<T, I> a) {
+  extern __shared__ float tile[];  // [16][N] fp32
+  const int64_t k = blockIdx.x;
+  const int64_t bk = k * a.kbig;
+  int64_t first_above, unused;
+  wg_lower_bound2([&](int64_t i) { return a.crp(i); }, 0, a.windows, bk + 1, bk + 1, first_above, unused);
+  const int64_t s = first_above - 1;
+  if (s < 0 || s >= a.windows) return;
+  const int64_t b0 = a.crp(s), b1 = a.crp(s + 1);
+  if (!(b1 - b0 > a.kbig && (b0 + a.kbig) / a.kbig == k)) return;
+  const int64_t k_end = (b1 - 1) / a.kbig;
+  const int64_t n = 16 * a.N;
+  for (int64_t i = threadIdx.x; i < n; i += blockDim.x) {
+    float acc = a.slots[(2 * k + 1) * n + i];
+    for (int64_t kk = k; kk <= k_end; ++kk) acc = acc + a.slots[(2 * kk) * n + i];
+    tile[i] = acc;
+  }
+  __syncthreads();
+  finish_window(a, s, tile);
+}
+
+template <typename T, typename I>
+spmm_status block_typed(const void* Crowptr, const void* Ccol, const void* Cvalue, int64_t windows,
+                        int64_t block_count, int64_t block_values, const void* Vrowptr,
                         int64_t vector_rows, int64_t vector_nnz, const void* dense, int64_t K,
-                        int64_t N, void* out, hipStream_t stream) {
+                        int64_t N, void* out, const float* vpart, float* slots, hipStream_t stream) {
   if (windows <= 0) return SPMM_OK;
+  BlockArgs<T, I> a;
+  a.Crowptr = static_cast<const I*>(Crowptr);
+  a.Ccol = static_cast<const I*>(Ccol);
+  a.Cvalue = static_cast<const T*>(Cvalue);
+  a.windows = windows;
   const int64_t limit = block_count < block_values / 16 ? block_count : block_values / 16;
+  a.limit = limit < 0 ? 0 : limit;
+  a.Vrowptr = static_cast<const I*>(Vrowptr);
+  a.vrows = vector_rows;
+  a.vnnz = vector_nnz;
+  a.dense = static_cast<const T*>(dense);
+  a.K = K;
+  a.N = N;
+  a.out = static_cast<T*>(out);
+  a.vpart = vpart;
+  a.slots = slots;
+  a.kbig = block_chunk<T>();
+  a.noverflow = block_overflow_ranges(a.limit, a.kbig);
+  a.per_xcd = ceil_div(windows, kXcds);
   const int64_t groups = (N + 63) / 64;
   const int waves = groups < 4 ? static_cast<int>(groups) : 4;
-  const int64_t per_xcd = ceil_div(windows, kXcds);
-  const int64_t grid = per_xcd * kXcds;
   const size_t lds = static_cast<size_t>(16) * N * sizeof(float);
-  hipLaunchKernelGGL((block_windows<T, I>), dim3(static_cast<unsigned>(grid)), dim3(64 * waves),
-                     lds, stream, static_cast<const I*>(Crowptr), static_cast<const I*>(Ccol),
-                     static_cast<const T*>(Cvalue), windows, limit < 0 ? 0 : limit,
-                     static_cast<const I*>(Vrowptr), static_cast<const I*>(Vcol),
-                     static_cast<const T*>(Vvalue), vector_rows, vector_nnz,
-                     static_cast<const T*>(dense), K, N, static_cast<T*>(out), per_xcd);
-  return check_launch("block_windows");
+  const int64_t grid = a.per_xcd * kXcds + a.noverflow;
+  hipLaunchKernelGGL((block_windows<T, I>), dim3(static_cast<unsigned>(grid)), dim3(64 * waves), lds,
+                     stream, a);
+  if (spmm_status st = check_launch("block_windows")) return st;
+  if (a.noverflow == 0) return SPMM_OK;
+  hipLaunchKernelGGL((block_combine<T, I>), dim3(static_cast<unsigned>(a.noverflow)), dim3(256), lds, stream,
+                     a);
+  return check_launch("block_combine");
 }
 
 }  // namespace
 
+int64_t block_overflow_ranges(int64_t blocks, int64_t kbig) {
+  return blocks > kbig ? ceil_div(blocks, kbig) : 0;
+}
+
 spmm_status launch_block(int32_t index_type, int32_t value_type, const void* Crowptr,
                          const void* Ccol, const void* Cvalue, int64_t windows,
                          int64_t block_count, int64_t block_values, const void* Vrowptr,
-                         const void* Vcol, const void* Vvalue, int64_t vector_rows,
-                         int64_t vector_nnz, const void* dense, int64_t dense_rows,
-                         int64_t width, void* out, hipStream_t stream) {
-#define SPMM_BLOCK_CALL(T, I)                                                                 \
+                         int64_t vector_rows, int64_t vector_nnz, const void* dense,
+                         int64_t dense_rows, int64_t width, void* out, const float* vpart,
+                         float* slots, hipStream_t stream) {
+#define SPMM_BLOCK_CALL(T, I)                                                                   \
   return block_typed<T, I>(Crowptr, Ccol, Cvalue, windows, block_count, block_values, Vrowptr, \
-                           Vcol, Vvalue, vector_rows, vector_nnz, dense, dense_rows, width, out, \
+                           vector_rows, vector_nnz, dense, dense_rows, width, out, vpart, slots, \
                            stream)
   if (value_type == SPMM_VALUE_F16) {
     if (index_type == SPMM_INDEX_I32) SPMM_BLOCK_CALL(_Float16, int32_t);

@@ -97,9 +97,9 @@ spmm_status spmm_csr_run(const spmm_csr_desc* d, const void* rowptr, const void*
       (d->dense_rows > 0 && dense == nullptr))
     return fail(SPMM_ERR_INVALID_ARGUMENT, "spmm_csr: null device pointer");
   if (spmm_status st = check_aligned(dense, out, "spmm_csr")) return st;
-  return launch_gather(d->index_type, d->value_type, rowptr, col, value, d->nnz, 0, d->rows,
-                       dense, d->dense_rows, d->width, out, workspace, workspace_bytes,
-                       as_stream(stream));
+  return launch_gather(d->index_type, d->value_type, rowptr, col, value, d->nnz, d->rows, 0, d->rows,
+                       dense, d->dense_rows, d->width, out, workspace, workspace_bytes, nullptr, 0, 0,
+                       nullptr, as_stream(stream));
 }
 
 int64_t spmm_mixed_out_rows(const spmm_mixed_desc* d) {
@@ -109,11 +109,32 @@ int64_t spmm_mixed_out_rows(const spmm_mixed_desc* d) {
   return blocks > vec ? blocks : vec;
 }
 
+namespace {
+// Workspace of the mixed operator: gather part, then the fp32 vector sums of
+// block-window rows ([16*windows][width]), then the pieces of windows longer
+// than the block chunk ([ranges][2][16][width]).
+struct MixedLayout {
+  size_t gather = 0, vpart = 0, slots = 0;
+  int64_t limit = 0;
+  explicit MixedLayout(const spmm_mixed_desc* d) {
+    const int64_t w = d->width > 0 ? d->width : 0;
+    gather = align_up(gather_workspace_bytes(d->vector_nnz < 0 ? 0 : d->vector_nnz, w), 256);
+    const int64_t windows = d->block_windows > 0 ? d->block_windows : 0;
+    vpart = align_up(static_cast<size_t>(16 * windows) * w * sizeof(float), 256);
+    limit = d->block_count < d->block_values / 16 ? d->block_count : d->block_values / 16;
+    if (limit < 0) limit = 0;
+    const int64_t ranges = block_overflow_ranges(limit, block_chunk_for(d->value_type));
+    slots = align_up(static_cast<size_t>(ranges * 2 * 16) * w * sizeof(float), 256);
+  }
+  size_t total() const { return gather + vpart + slots; }
+};
+}  // namespace
+
 spmm_status spmm_mixed_workspace(const spmm_mixed_desc* d, size_t* bytes) {
   clear_error();
   if (d == nullptr || bytes == nullptr) return fail(SPMM_ERR_INVALID_ARGUMENT, "null argument");
   if (spmm_status st = check_types(d->index_type, d->value_type, "spmm_ascend_cube")) return st;
-  *bytes = gather_workspace_bytes(d->vector_nnz < 0 ? 0 : d->vector_nnz, d->width);
+  *bytes = MixedLayout(d).total();
   return SPMM_OK;
 }
 
@@ -133,22 +154,28 @@ spmm_status spmm_mixed_run(const spmm_mixed_desc* d, const void* Crowptr, const 
   if (out == nullptr || (d->dense_rows > 0 && dense == nullptr) ||
       (d->block_windows > 0 && Crowptr == nullptr) ||
       (d->block_count > 0 && (Ccol == nullptr || Cvalue == nullptr)) ||
-      (d->vector_rows > 0 && Vrowptr == nullptr) ||
+      Vrowptr == nullptr ||
       (d->vector_nnz > 0 && (Vcol == nullptr || Vvalue == nullptr)))
     return fail(SPMM_ERR_INVALID_ARGUMENT, "spmm_ascend_cube: null device pointer");
   if (spmm_status st = check_aligned(dense, out, "spmm_ascend_cube")) return st;
   hipStream_t s = as_stream(stream);
-  const int64_t block_rows = 16 * d->block_windows;
-  spmm_status st =
-      launch_block(d->index_type, d->value_type, Crowptr, Ccol, Cvalue, d->block_windows,
-                   d->block_count, d->block_values, Vrowptr, Vcol, Vvalue, d->vector_rows,
-                   d->vector_nnz, dense, d->dense_rows, d->width, out, s);
+  const MixedLayout lay(d);
+  if (workspace == nullptr || workspace_bytes < lay.total())
+    return fail(SPMM_ERR_CONTRACT, "spmm_ascend_cube: workspace too small: need " +
+                                       std::to_string(lay.total()) + " bytes");
+  char* ws = static_cast<char*>(workspace);
+  float* vpart = reinterpret_cast<float*>(ws + lay.gather);
+  float* slots = reinterpret_cast<float*>(ws + lay.gather + lay.vpart);
+  // Vector pass first (it leaves the fp32 vector sums of block-window rows in
+  // vpart), then the block part, which adds them and rounds once.
+  spmm_status st = launch_gather(d->index_type, d->value_type, Vrowptr, Vcol, Vvalue, d->vector_nnz,
+                                 d->vector_rows, 0, out_rows, dense, d->dense_rows, d->width, out, ws,
+                                 lay.gather, d->block_windows > 0 ? Crowptr : nullptr, d->block_windows,
+                                 lay.limit, vpart, s);
   if (st != SPMM_OK) return st;
-  if (d->vector_rows > block_rows)
-    st = launch_gather(d->index_type, d->value_type, Vrowptr, Vcol, Vvalue, d->vector_nnz,
-                       block_rows, d->vector_rows, dense, d->dense_rows, d->width, out,
-                       workspace, workspace_bytes, s);
-  return st;
+  return launch_block(d->index_type, d->value_type, Crowptr, Ccol, Cvalue, d->block_windows,
+                      d->block_count, d->block_values, Vrowptr, d->vector_rows, d->vector_nnz, dense,
+                      d->dense_rows, d->width, out, vpart, slots, s);
 }
 
 }  // extern "C"

@@ -29,6 +29,7 @@
 //    partials in range order.
 #include "common.h"
 #include "lanevec.h"
+#include "wgsearch.h"
 
 namespace spmm {
 namespace {
@@ -48,66 +49,35 @@ template <typename I>
 struct Geometry {
   const I* rowptr;
   int64_t* tail;           // [nranges]: row that starts in range j and runs past its end, or -1
-  int64_t row_lo, row_hi;  // vector rows handled
+  int64_t row_lo, row_hi;  // rows handled
+  int64_t vrows;           // rowptr holds vrows + 1 entries; rows >= vrows are empty
   int64_t nnz;             // extent of col[] / value[]
   int64_t nranges;         // max(1, ceil(nnz / R))
+  // Block part of the mixed operator (cwin == 0 for spmm_csr): the vector sum
+  // of a row in a block window that has blocks goes to vpart in fp32 (the
+  // block kernel, run afterwards, adds it to the block sum and rounds once);
+  // such rows are otherwise left to the block kernel.
+  const I* Crowptr;
+  int64_t cwin, climit;
+  float* vpart;
 
   __device__ inline int64_t rp(int64_t r) const {
-    return clampi(static_cast<int64_t>(rowptr[r]), 0, nnz);
+    return clampi(static_cast<int64_t>(rowptr[r < vrows ? r : vrows]), 0, nnz);
   }
   __device__ inline int64_t lo(int64_t j) const { return j * kGatherRange; }
   __device__ inline int64_t hi(int64_t j) const {
     const int64_t h = (j + 1) * kGatherRange;
     return h < nnz ? h : nnz;
   }
-};
-
-// Work-group search: first row r in [row_lo, row_hi] with rp(r) >= pos (row_hi
-// if none), for two positions at once (one per half of the work-group).  Each
-// round probes `half` evenly spaced rows and keeps the bracket of the first
-// hit, so a 100k-row pointer takes three rounds of one load per thread instead
-// of a 17-step chain of dependent loads.
-template <typename I>
-__device__ inline void wg_lower_rows(const Geometry<I>& g, int64_t posA, int64_t posB,
-                                     int64_t& outA, int64_t& outB) {
-  __shared__ int s_min[2];
-  __shared__ int64_t s_ans[2];
-  const int half = blockDim.x >> 1;
-  const int q = threadIdx.x >= half ? 1 : 0;
-  const int k = threadIdx.x - q * half;
-  const int64_t pos = q ? posB : posA;
-  int64_t lo = g.row_lo, hi = g.row_hi;
-  bool done = false;
-  for (int round = 0; round < 12; ++round) {
-    if (threadIdx.x < 2) s_min[threadIdx.x] = INT32_MAX;
-    __syncthreads();
-    const int64_t n = hi - lo;
-    const bool final_round = n <= half;
-    if (!done) {
-      const int64_t r = final_round ? lo + k : lo + (n * (k + 1)) / (half + 1);
-      if ((!final_round || k < n) && g.rp(r) >= pos) atomicMin(&s_min[q], k);
-    }
-    __syncthreads();
-    if (!done) {
-      const int km = s_min[q];
-      if (final_round) {
-        if (km != INT32_MAX) hi = lo + km;
-        done = true;
-      } else if (km == INT32_MAX) {
-        lo = lo + (n * half) / (half + 1) + 1;
-      } else {
-        const int64_t rk = lo + (n * (km + 1)) / (half + 1);
-        lo = km == 0 ? lo : lo + (n * km) / (half + 1) + 1;
-        hi = rk;
-      }
-    }
-    if (__syncthreads_and(done)) break;
+  __device__ inline int64_t crp(int64_t s) const {
+    return clampi(static_cast<int64_t>(Crowptr[s]), 0, climit);
   }
-  if (k == 0) s_ans[q] = hi;
-  __syncthreads();
-  outA = s_ans[0];
-  outB = s_ans[1];
-}
+  // Row r lies in a block window that has blocks.
+  __device__ inline bool in_block_window(int64_t r) const {
+    const int64_t s = r / 16;
+    return s < cwin && crp(s + 1) > crp(s);
+  }
+};
 
 // One batch of kBatch consecutive nonzeros: raw 16-byte dense pieces, values
 // and column validity.
@@ -143,17 +113,20 @@ struct Stream {
 };
 
 // Accumulates batches in position order.  Per tile position the LDS mark is
-// (row + 1 - tA) << 1 | ends_here, where the row part is set only at the
-// position a row starts: it tracks the current row and flushes at row ends.
+// (row + 1 - rS) << 2 | to_vpart << 1 | ends_here, where the row part is set
+// only at the position a row starts: it tracks the current row, routes rows
+// of block windows to vpart, and flushes at row ends.
 template <typename T>
 struct Sink {
   const int32_t* s_mark;
-  int64_t P0, pe, tA, row_hi;
+  int64_t P0, pe, rS, row_hi;
   T* out;
   int64_t N, c0;
+  float* vpart;
   float* head_slot;
   float* tail_slot;
   int64_t row;             // row in progress, -1 while it is one started before the range
+  bool to_vpart;           // the row in progress belongs to a block window
   bool last_ended;         // the last consumed position ended its row
   float acc[lanes::LaneVec<T>::V];
 
@@ -164,7 +137,10 @@ struct Sink {
       const int64_t p = p0 + u;
       if (p < pe) {
         const int32_t m = s_mark[p - P0];
-        if (m >> 1) row = tA + (m >> 1) - 1;
+        if (m >> 2) {
+          row = rS + (m >> 2) - 1;
+          to_vpart = m & 2;
+        }
         float x[V];
         lanes::LaneVec<T>::unpack(b.x[u], x);
 #pragma unroll
@@ -178,7 +154,13 @@ struct Sink {
 #pragma unroll
             for (int i = 0; i < V; ++i) head_slot[i] = acc[i];
           } else if (row < row_hi) {
-            lanes::LaneVec<T>::store(out + row * N + c0, acc);
+            if (to_vpart) {
+              float* dst = vpart + row * N + c0;
+#pragma unroll
+              for (int i = 0; i < V; ++i) dst[i] = acc[i];
+            } else {
+              lanes::LaneVec<T>::store(out + row * N + c0, acc);
+            }
           }
 #pragma unroll
           for (int i = 0; i < V; ++i) acc[i] = 0.f;
@@ -217,10 +199,12 @@ __global__ __launch_bounds__(kWgThreads) void gather_tiles(
   const bool last_tile = j1 == g.nranges;
   const int64_t base = g.rp(g.row_lo), end = g.rp(g.row_hi);
 
-  // Rows starting in the tile: [tA, rB) (rB = first row starting at or after P1).
-  int64_t tA, rB;
-  wg_lower_rows(g, P0, P1, tA, rB);
-  if (last_tile) rB = g.row_hi;
+  // Rows overlapping the tile: [rS, rE) with rS = the last row whose end is
+  // at most P0 (first row with rp >= P0+1, minus one) and rE = the first row
+  // with rp >= P1+1.  Runs of empty rows before the tile are skipped.
+  int64_t rS, rE;
+  wg_lower_bound2([&](int64_t r) { return g.rp(r); }, g.row_lo, g.row_hi, P0 + 1, P1 + 1, rS, rE);
+  rS = rS - 1 > g.row_lo ? rS - 1 : g.row_lo;
 
   // Stage the tile's nonzeros of our rows ([base, end)) and clear the marks;
   // each thread issues its loads before the first LDS store.
@@ -251,26 +235,18 @@ __global__ __launch_bounds__(kWgThreads) void gather_tiles(
     }
   }
   __syncthreads();
-  // Mark the starts and ends of the tile's non-empty rows (each position is
-  // marked only by the row that holds it; row tA-1 may start before the tile
-  // and end in it).  Write the empty rows the tile owns (those whose start
-  // lies in the tile, or at/after it for the last tile).
-  const int64_t r0 = tA - 1 > g.row_lo ? tA - 1 : g.row_lo;
-  for (int64_t r = r0 + threadIdx.x; r < rB; r += blockDim.x) {
+  // Mark the starts and ends of the tile's non-empty rows; each position is
+  // marked only by the row that holds it.  Empty rows are left to the post pass.
+  for (int64_t r = rS + threadIdx.x; r < rE; r += blockDim.x) {
     const int64_t a = g.rp(r), b = g.rp(r + 1);
     if (a < b) {
-      const bool start_in = a >= P0 && a < P1 && r >= tA && r - tA < INT32_MAX - 1;
+      const bool start_in = a >= P0 && a < P1 && r - rS < (INT32_MAX >> 2) - 1;
       const bool end_in = b - 1 >= P0 && b - 1 < P1;
-      if (start_in) s_mark[a - P0] = static_cast<int32_t>((r - tA + 1) << 1) | (end_in && b - 1 == a ? 1 : 0);
-      if (end_in && !(start_in && b - 1 == a)) s_mark[b - 1 - P0] = 1;
-    } else if (r >= tA && a >= P0 && (a < P1 || last_tile)) {
-      T* dst = out + r * N;
-      for (int64_t c = 0; c < N; c += V) {
-        float z[V];
-#pragma unroll
-        for (int i = 0; i < V; ++i) z[i] = 0.f;
-        LaneVec<T>::store(dst + c, z);
+      if (start_in) {
+        const int32_t vp = g.in_block_window(r) ? 2 : 0;
+        s_mark[a - P0] = static_cast<int32_t>((r - rS + 1) << 2) | vp | (end_in && b - 1 == a ? 1 : 0);
       }
+      if (end_in && !(start_in && b - 1 == a)) s_mark[b - 1 - P0] = 1;
     }
   }
   __syncthreads();
@@ -296,12 +272,14 @@ __global__ __launch_bounds__(kWgThreads) void gather_tiles(
   sk.s_mark = s_mark;
   sk.P0 = P0;
   sk.pe = pe;
-  sk.tA = tA;
+  sk.rS = rS;
   sk.row_hi = g.row_hi;
   sk.last_ended = false;
   sk.out = out;
   sk.N = N;
   sk.c0 = c0;
+  sk.vpart = g.vpart;
+  sk.to_vpart = false;
   sk.head_slot = ws + (2 * j) * slot + c0;
   sk.tail_slot = ws + (2 * j + 1) * slot + c0;
   sk.row = -1;  // set by the first row-start mark; stays -1 for a row begun earlier
@@ -344,70 +322,106 @@ __global__ __launch_bounds__(kWgThreads) void gather_tiles(
   if (reporter) g.tail[j] = tail_row;
 }
 
-// Adds the partials of every row that crosses range ends, in range order.
+// Post pass, one launch:
+//  * work-groups [0, fix_blocks): add the partials of every row that crosses
+//    range ends, in range order (lane group per (range, column chunk));
+//  * the rest: empty rows, 64 per wavefront, are written as zeros (rows of
+//    block windows with blocks are left to the block kernel).
 template <typename T, typename I>
-__global__ __launch_bounds__(kWgThreads) void gather_fixup(Geometry<I> g, int64_t N, T* __restrict__ out,
-                                                           const float* __restrict__ ws, int log2L,
-                                                           int64_t chunks, int64_t slot) {
+__global__ __launch_bounds__(kWgThreads) void gather_post(Geometry<I> g, int64_t N, T* __restrict__ out,
+                                                          const float* __restrict__ ws, int log2L,
+                                                          int64_t chunks, int64_t slot, int64_t fix_blocks) {
   constexpr int V = LaneVec<T>::V;
-  const int L = 1 << log2L;
-  const int64_t tid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  const int64_t item = tid >> log2L;
-  const int lane = static_cast<int>(tid & (L - 1));
-  if (item >= (g.nranges - 1) * chunks) return;
-  const int64_t j = item / chunks;
-  const int64_t cc = item - j * chunks;
-  const int64_t c0 = (cc * L + lane) * V;
-  if (c0 >= N) return;
+  if (static_cast<int64_t>(blockIdx.x) < fix_blocks) {
+    const int L = 1 << log2L;
+    const int64_t tid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int64_t item = tid >> log2L;
+    const int lane = static_cast<int>(tid & (L - 1));
+    if (item >= (g.nranges - 1) * chunks) return;
+    const int64_t j = item / chunks;
+    const int64_t cc = item - j * chunks;
+    const int64_t c0 = (cc * L + lane) * V;
+    if (c0 >= N) return;
+    const int64_t r = g.tail[j];
+    if (r < g.row_lo || r >= g.row_hi) return;  // no row starts in range j and continues
+    const int64_t stop = g.rp(r + 1);
 
-  const int64_t r = g.tail[j];
-  if (r < g.row_lo || r >= g.row_hi) return;  // no row starts in range j and continues
-  const int64_t stop = g.rp(r + 1);
-
-  float acc[V];
-  const float* src = ws + (2 * j + 1) * slot + c0;
+    float acc[V];
+    const float* src = ws + (2 * j + 1) * slot + c0;
 #pragma unroll
-  for (int i = 0; i < V; ++i) acc[i] = src[i];
-  // Head partials of ranges j+1 .. k_end-1, read 8 at a time, added in order.
-  int64_t k_end = (stop + kGatherRange - 1) / kGatherRange;
-  if (k_end > g.nranges) k_end = g.nranges;
-  constexpr int kFix = 8;
-  for (int64_t k0 = j + 1; k0 < k_end; k0 += kFix) {
-    lanes::raw16_t h[kFix][(V * 4 + 15) / 16];
+    for (int i = 0; i < V; ++i) acc[i] = src[i];
+    // Head partials of ranges j+1 .. k_end-1, read 8 at a time, added in order.
+    int64_t k_end = (stop + kGatherRange - 1) / kGatherRange;
+    if (k_end > g.nranges) k_end = g.nranges;
+    constexpr int kFix = 8;
+    for (int64_t k0 = j + 1; k0 < k_end; k0 += kFix) {
+      lanes::raw16_t h[kFix][(V * 4 + 15) / 16];
 #pragma unroll
-    for (int u = 0; u < kFix; ++u) {
-      const int64_t k = k0 + u < k_end ? k0 + u : k_end - 1;
-      const float* hp = ws + (2 * k) * slot + c0;
+      for (int u = 0; u < kFix; ++u) {
+        const int64_t k = k0 + u < k_end ? k0 + u : k_end - 1;
+        const float* hp = ws + (2 * k) * slot + c0;
 #pragma unroll
-      for (int w = 0; w < (V * 4 + 15) / 16; ++w) h[u][w] = lanes::load_raw16(hp + 4 * w);
-    }
+        for (int w = 0; w < (V * 4 + 15) / 16; ++w) h[u][w] = lanes::load_raw16(hp + 4 * w);
+      }
 #pragma unroll
-    for (int u = 0; u < kFix; ++u) {
-      if (k0 + u < k_end) {
+      for (int u = 0; u < kFix; ++u) {
+        if (k0 + u < k_end) {
 #pragma unroll
-        for (int w = 0; w < (V * 4 + 15) / 16; ++w) {
-          const lanes::float4_t f = __builtin_bit_cast(lanes::float4_t, h[u][w]);
+          for (int w = 0; w < (V * 4 + 15) / 16; ++w) {
+            const lanes::float4_t f = __builtin_bit_cast(lanes::float4_t, h[u][w]);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) acc[4 * w + i] = acc[4 * w + i] + f[i];
+            for (int i = 0; i < 4; ++i) acc[4 * w + i] = acc[4 * w + i] + f[i];
+          }
         }
       }
     }
+    if (g.in_block_window(r)) {
+      float* dst = g.vpart + r * N + c0;
+#pragma unroll
+      for (int i = 0; i < V; ++i) dst[i] = acc[i];
+    } else {
+      LaneVec<T>::store(out + r * N + c0, acc);
+    }
+    return;
   }
-  LaneVec<T>::store(out + r * N + c0, acc);
+  // Empty rows: wavefront w takes rows [row_lo + 64w, +64).
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = (static_cast<int64_t>(blockIdx.x) - fix_blocks) * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int64_t r = g.row_lo + wave * 64 + lane;
+  // Rows of block windows with blocks are written by the block kernel.
+  const bool zero_row = r < g.row_hi && g.rp(r) == g.rp(r + 1) && !g.in_block_window(r);
+  unsigned long long pending = __ballot(zero_row);
+  while (pending) {
+    const int src_lane = __ffsll(static_cast<long long>(pending)) - 1;
+    pending &= pending - 1;
+    const int64_t rr = g.row_lo + wave * 64 + src_lane;
+    for (int64_t c0 = static_cast<int64_t>(lane) * V; c0 < N; c0 += 64 * V) {
+      float z[V];
+#pragma unroll
+      for (int i = 0; i < V; ++i) z[i] = 0.f;
+      LaneVec<T>::store(out + rr * N + c0, z);
+    }
+  }
 }
 
 template <typename T, typename I>
 spmm_status gather_typed(const void* rowptr, const void* col, const void* value, int64_t nnz,
-                         int64_t row_lo, int64_t row_hi, const void* dense, int64_t K,
-                         int64_t N, void* out, void* ws, size_t ws_bytes, hipStream_t stream) {
+                         int64_t vrows, int64_t row_lo, int64_t row_hi, const void* dense, int64_t K,
+                         int64_t N, void* out, void* ws, size_t ws_bytes, const void* Crowptr,
+                         int64_t cwin, int64_t climit, float* vpart, hipStream_t stream) {
   constexpr int V = LaneVec<T>::V;
   if (row_hi <= row_lo) return SPMM_OK;
   Geometry<I> g;
   g.rowptr = static_cast<const I*>(rowptr);
   g.row_lo = row_lo;
   g.row_hi = row_hi;
+  g.vrows = vrows;
   g.nnz = nnz < 0 ? 0 : nnz;
   g.nranges = g.nnz > 0 ? ceil_div(g.nnz, kGatherRange) : 1;
+  g.Crowptr = static_cast<const I*>(Crowptr);
+  g.cwin = Crowptr ? cwin : 0;
+  g.climit = climit;
+  g.vpart = vpart;
 
   const int64_t lanes_needed = N / V;
   int log2L = 0;
@@ -431,21 +445,24 @@ spmm_status gather_typed(const void* rowptr, const void* col, const void* value,
   g.tail = static_cast<int64_t*>(ws);
   float* partial = reinterpret_cast<float*>(static_cast<char*>(ws) + tail_bytes);
 
-  const int64_t tiles = ceil_div(g.nranges, ranges_per_tile);
-  const size_t lds = static_cast<size_t>(ranges_per_tile * kGatherRange) *
-                     (sizeof(I) + sizeof(T) + sizeof(int32_t));
-  hipLaunchKernelGGL((gather_tiles<T, I>), dim3(static_cast<unsigned>(tiles)),
-                     dim3(static_cast<unsigned>(wg_threads)), lds, stream, g,
-                     static_cast<const I*>(col), static_cast<const T*>(value),
-                     static_cast<const T*>(dense), K, N, static_cast<T*>(out), partial, log2L,
-                     chunks, ranges_per_tile, slot);
-  spmm_status st = check_launch("gather_tiles");
-  if (st != SPMM_OK || g.nranges < 2) return st;
-  const int64_t fthreads = (g.nranges - 1) * chunks * L;
-  hipLaunchKernelGGL((gather_fixup<T, I>), dim3(static_cast<unsigned>(ceil_div(fthreads, kWgThreads))),
+  if (g.nnz > 0) {
+    const int64_t tiles = ceil_div(g.nranges, ranges_per_tile);
+    const size_t lds = static_cast<size_t>(ranges_per_tile * kGatherRange) *
+                       (sizeof(I) + sizeof(T) + sizeof(int32_t));
+    hipLaunchKernelGGL((gather_tiles<T, I>), dim3(static_cast<unsigned>(tiles)),
+                       dim3(static_cast<unsigned>(wg_threads)), lds, stream, g,
+                       static_cast<const I*>(col), static_cast<const T*>(value),
+                       static_cast<const T*>(dense), K, N, static_cast<T*>(out), partial, log2L,
+                       chunks, ranges_per_tile, slot);
+    if (spmm_status st = check_launch("gather_tiles")) return st;
+  }
+  const int64_t fix_items = g.nnz > 0 ? (g.nranges - 1) * chunks * L : 0;
+  const int64_t fix_blocks = ceil_div(fix_items, kWgThreads);
+  const int64_t row_blocks = ceil_div(ceil_div(row_hi - row_lo, 64), kWgThreads / 64);
+  hipLaunchKernelGGL((gather_post<T, I>), dim3(static_cast<unsigned>(fix_blocks + row_blocks)),
                      dim3(kWgThreads), 0, stream, g, N, static_cast<T*>(out),
-                     static_cast<const float*>(partial), log2L, chunks, slot);
-  return check_launch("gather_fixup");
+                     static_cast<const float*>(partial), log2L, chunks, slot, fix_blocks);
+  return check_launch("gather_post");
 }
 
 }  // namespace
@@ -457,25 +474,22 @@ size_t gather_workspace_bytes(int64_t nnz, int64_t width) {
 }
 
 spmm_status launch_gather(int32_t index_type, int32_t value_type, const void* rowptr,
-                          const void* col, const void* value, int64_t nnz, int64_t row_lo,
-                          int64_t row_hi, const void* dense, int64_t dense_rows, int64_t width,
-                          void* out, void* workspace, size_t workspace_bytes,
+                          const void* col, const void* value, int64_t nnz, int64_t vrows,
+                          int64_t row_lo, int64_t row_hi, const void* dense, int64_t dense_rows,
+                          int64_t width, void* out, void* workspace, size_t workspace_bytes,
+                          const void* Crowptr, int64_t cwin, int64_t climit, float* vpart,
                           hipStream_t stream) {
+#define SPMM_GATHER_CALL(T, I)                                                                 \
+  return gather_typed<T, I>(rowptr, col, value, nnz, vrows, row_lo, row_hi, dense, dense_rows, \
+                            width, out, workspace, workspace_bytes, Crowptr, cwin, climit, vpart, \
+                            stream)
   if (value_type == SPMM_VALUE_F16) {
-    if (index_type == SPMM_INDEX_I32)
-      return gather_typed<_Float16, int32_t>(rowptr, col, value, nnz, row_lo, row_hi, dense,
-                                             dense_rows, width, out, workspace, workspace_bytes,
-                                             stream);
-    return gather_typed<_Float16, int64_t>(rowptr, col, value, nnz, row_lo, row_hi, dense,
-                                           dense_rows, width, out, workspace, workspace_bytes,
-                                           stream);
+    if (index_type == SPMM_INDEX_I32) SPMM_GATHER_CALL(_Float16, int32_t);
+    SPMM_GATHER_CALL(_Float16, int64_t);
   }
-  if (index_type == SPMM_INDEX_I32)
-    return gather_typed<float, int32_t>(rowptr, col, value, nnz, row_lo, row_hi, dense,
-                                        dense_rows, width, out, workspace, workspace_bytes,
-                                        stream);
-  return gather_typed<float, int64_t>(rowptr, col, value, nnz, row_lo, row_hi, dense, dense_rows,
-                                      width, out, workspace, workspace_bytes, stream);
+  if (index_type == SPMM_INDEX_I32) SPMM_GATHER_CALL(float, int32_t);
+  SPMM_GATHER_CALL(float, int64_t);
+#undef SPMM_GATHER_CALL
 }
 
 }  // namespace spmm
