@@ -31,14 +31,23 @@ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
-// Split length of the CSR gather path: nonzero positions are cut into ranges
-// [j*R, (j+1)*R).  It is a constant of the build, independent of width and
-// dtype, which is what makes the gather results identical for every feature
-// width.
-#ifndef SPMM_GATHER_RANGE
-#define SPMM_GATHER_RANGE 256
+// Split length R of the CSR gather path: nonzero positions are cut into
+// ranges [j*R, (j+1)*R), one lane group per range.  R is the largest power of
+// two in [kGatherRangeMin, kGatherRangeMax] with about nnz / R >=
+// kGatherSplit ranges, so small matrices still run enough lane groups at once
+// to cover memory latency.  It depends on nnz only (not on width or dtype),
+// which is what makes the gather results identical for every feature width.
+#ifndef SPMM_GATHER_SPLIT
+#define SPMM_GATHER_SPLIT 24576
 #endif
-constexpr int64_t kGatherRange = SPMM_GATHER_RANGE;
+constexpr int64_t kGatherSplit = SPMM_GATHER_SPLIT;
+constexpr int64_t kGatherRangeMin = 16;
+constexpr int64_t kGatherRangeMax = 256;
+inline int64_t gather_range(int64_t nnz) {
+  int64_t r = kGatherRangeMin;
+  while (r < kGatherRangeMax && 2 * r * kGatherSplit <= nnz) r *= 2;
+  return r;
+}
 
 // fp32 storage of one partial row in the gather workspace, padded so every
 // slot starts 256-byte aligned.

@@ -7,12 +7,14 @@
 // accumulated in fp32 and rounded once to the output type.
 //
 // Work decomposition (MI355X-native, not the reference's 40-core split):
-//  * Nonzero positions are cut into fixed ranges [j*R, (j+1)*R) with
-//    R = kGatherRange.  A "lane group" of L lanes (each lane owns 16 bytes of
-//    an output row: L = width/8 for fp16, width/4 for fp32, capped at 64)
-//    processes one range.  Cut points depend only on the positions, so every
-//    output element sees the same fp32 operation sequence for every width N:
-//    results are deterministic and bit-identical across widths.
+//  * Nonzero positions are cut into fixed ranges [j*R, (j+1)*R), where R is
+//    a power of two chosen from nnz alone (gather_range: small matrices get
+//    short ranges so that enough lane groups run at once).  A "lane group" of
+//    L lanes (each lane owns 16 bytes of an output row: L = width/8 for fp16,
+//    width/4 for fp32, capped at 64) processes one range.  Cut points depend
+//    only on the positions and nnz, so every output element sees the same
+//    fp32 operation sequence for every width N: results are deterministic and
+//    bit-identical across widths.
 //  * gather_tiles: a work-group takes a tile of consecutive ranges.  It finds
 //    the rows starting in the tile with a work-group-wide many-way search of
 //    the row pointer (a few rounds of one load per thread instead of a chain
@@ -43,7 +45,11 @@ constexpr int kWgThreads = 256;
 #endif
 constexpr int kBatch = SPMM_GATHER_BATCH;  // dense rows per batch (two batches in flight)
 constexpr int kStageUnroll = 8;             // staging loads issued per thread before storing
-constexpr int64_t kTilePositions = 4096;    // nonzeros staged per work-group
+#ifndef SPMM_GATHER_TILE_RANGES
+#define SPMM_GATHER_TILE_RANGES 16
+#endif
+// Ranges per work-group tile (the tile stages ranges * R nonzeros in LDS).
+constexpr int64_t kTileRanges = SPMM_GATHER_TILE_RANGES;
 
 template <typename I>
 struct Geometry {
@@ -52,6 +58,7 @@ struct Geometry {
   int64_t row_lo, row_hi;  // rows handled
   int64_t vrows;           // rowptr holds vrows + 1 entries; rows >= vrows are empty
   int64_t nnz;             // extent of col[] / value[]
+  int64_t range;           // R, positions per range
   int64_t nranges;         // max(1, ceil(nnz / R))
   // Block part of the mixed operator (cwin == 0 for spmm_csr): the vector sum
   // of a row in a block window that has blocks goes to vpart in fp32 (the
@@ -64,9 +71,9 @@ struct Geometry {
   __device__ inline int64_t rp(int64_t r) const {
     return clampi(static_cast<int64_t>(rowptr[r < vrows ? r : vrows]), 0, nnz);
   }
-  __device__ inline int64_t lo(int64_t j) const { return j * kGatherRange; }
+  __device__ inline int64_t lo(int64_t j) const { return j * range; }
   __device__ inline int64_t hi(int64_t j) const {
-    const int64_t h = (j + 1) * kGatherRange;
+    const int64_t h = (j + 1) * range;
     return h < nnz ? h : nnz;
   }
   __device__ inline int64_t crp(int64_t s) const {
@@ -79,34 +86,40 @@ struct Geometry {
   }
 };
 
-// One batch of kBatch consecutive nonzeros: raw 16-byte dense pieces, values
-// and column validity.
+// One batch of kBatch consecutive nonzeros: raw 16-byte dense pieces, values,
+// row marks (0 past the range end) and column validity.
 template <typename T>
 struct Batch {
   lanes::raw16_t x[kBatch];
   float v[kBatch];
+  int32_t m[kBatch];
   bool ok[kBatch];
 };
 
-// Issues the dense loads of a batch from the LDS-staged column ids.
+// Issues the dense loads of a batch from the LDS-staged column ids; the row
+// marks are read from LDS here too, so accumulation never waits on LDS.
 template <typename T, typename I>
 struct Stream {
   const I* s_col;
   const T* s_val;
+  const int32_t* s_mark;
   const T* dense;
   int64_t K, N, c0, P0, pe;
 
   // Branch-free so the loads of a batch stay in flight together: positions
   // past the range end and invalid columns load dense row 0 (K >= 1 here)
-  // and are masked out by `ok`.
+  // and are masked out by `ok`; positions past the range end get mark 0.
   __device__ inline void issue(Batch<T>& b, int64_t p0) const {
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
       const int64_t p = p0 + u;
-      const int64_t q = (p < pe ? p : pe - 1) - P0;
+      const bool in = p < pe;
+      const int64_t q = (in ? p : pe - 1) - P0;
       const int64_t c = static_cast<int64_t>(s_col[q]);
+      const int32_t m = s_mark[q];
       b.v[u] = static_cast<float>(s_val[q]);
-      b.ok[u] = p < pe && static_cast<uint64_t>(c) < static_cast<uint64_t>(K);
+      b.m[u] = in ? m : 0;
+      b.ok[u] = in && static_cast<uint64_t>(c) < static_cast<uint64_t>(K);
       b.x[u] = lanes::load_raw16(dense + (b.ok[u] ? c : 0) * N + c0);
     }
   }
@@ -127,44 +140,38 @@ struct Sink {
   float* tail_slot;
   int64_t row;             // row in progress, -1 while it is one started before the range
   bool to_vpart;           // the row in progress belongs to a block window
-  bool last_ended;         // the last consumed position ended its row
   float acc[lanes::LaneVec<T>::V];
 
-  __device__ inline void consume(const Batch<T>& b, int64_t p0) {
+  // Positions past the range end carry mark 0 and ok = false: no-ops.
+  __device__ inline void consume(const Batch<T>& b) {
     constexpr int V = lanes::LaneVec<T>::V;
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
-      const int64_t p = p0 + u;
-      if (p < pe) {
-        const int32_t m = s_mark[p - P0];
-        if (m >> 2) {
-          row = rS + (m >> 2) - 1;
-          to_vpart = m & 2;
-        }
-        float x[V];
-        lanes::LaneVec<T>::unpack(b.x[u], x);
+      const int32_t m = b.m[u];
+      const int32_t start = m >> 2;
+      row = start ? rS + start - 1 : row;
+      to_vpart = start ? (m & 2) != 0 : to_vpart;
+      float x[V];
+      lanes::LaneVec<T>::unpack(b.x[u], x);
 #pragma unroll
-        for (int i = 0; i < V; ++i) {
-          const float t = __builtin_fmaf(b.v[u], x[i], acc[i]);
-          acc[i] = b.ok[u] ? t : acc[i];
-        }
-        last_ended = m & 1;
-        if (last_ended) {
-          if (row < 0) {
+      for (int i = 0; i < V; ++i) {
+        const float t = __builtin_fmaf(b.v[u], x[i], acc[i]);
+        acc[i] = b.ok[u] ? t : acc[i];
+      }
+      if (m & 1) {
+        // fp32 destinations: the head slot (row begun before the range) and
+        // vpart (block-window rows); others are rounded into out.
+        if (row < row_hi) {
+          if (row < 0 || to_vpart) {
+            float* dst = row < 0 ? head_slot : vpart + row * N + c0;
 #pragma unroll
-            for (int i = 0; i < V; ++i) head_slot[i] = acc[i];
-          } else if (row < row_hi) {
-            if (to_vpart) {
-              float* dst = vpart + row * N + c0;
-#pragma unroll
-              for (int i = 0; i < V; ++i) dst[i] = acc[i];
-            } else {
-              lanes::LaneVec<T>::store(out + row * N + c0, acc);
-            }
+            for (int i = 0; i < V; ++i) dst[i] = acc[i];
+          } else {
+            lanes::LaneVec<T>::store(out + row * N + c0, acc);
           }
-#pragma unroll
-          for (int i = 0; i < V; ++i) acc[i] = 0.f;
         }
+#pragma unroll
+        for (int i = 0; i < V; ++i) acc[i] = 0.f;
       }
     }
   }
@@ -173,7 +180,7 @@ struct Sink {
   // returns that row if it started in this range (a tail), else -1.
   __device__ inline int64_t finish() {
     constexpr int V = lanes::LaneVec<T>::V;
-    if (last_ended) return -1;
+    if (s_mark[pe - 1 - P0] & 1) return -1;
     float* dst = row < 0 ? head_slot : tail_slot;
 #pragma unroll
     for (int i = 0; i < V; ++i) dst[i] = acc[i];
@@ -188,7 +195,7 @@ __global__ __launch_bounds__(kWgThreads) void gather_tiles(
     int log2L, int64_t chunks, int64_t ranges_per_tile, int64_t slot) {
   constexpr int V = LaneVec<T>::V;
   extern __shared__ __align__(16) unsigned char smem[];
-  const int64_t tile_positions = ranges_per_tile * kGatherRange;
+  const int64_t tile_positions = ranges_per_tile * g.range;
   I* s_col = reinterpret_cast<I*>(smem);
   T* s_val = reinterpret_cast<T*>(smem + tile_positions * sizeof(I));
   int32_t* s_mark = reinterpret_cast<int32_t*>(smem + tile_positions * (sizeof(I) + sizeof(T)));
@@ -274,7 +281,6 @@ __global__ __launch_bounds__(kWgThreads) void gather_tiles(
   sk.pe = pe;
   sk.rS = rS;
   sk.row_hi = g.row_hi;
-  sk.last_ended = false;
   sk.out = out;
   sk.N = N;
   sk.c0 = c0;
@@ -295,7 +301,12 @@ __global__ __launch_bounds__(kWgThreads) void gather_tiles(
       z.v[u] = 0.f;
       z.x[u] = lanes::raw16_t{0, 0, 0, 0};
     }
-    for (int64_t p0 = ps; p0 < pe; p0 += kBatch) sk.consume(z, p0);
+    for (int u = 0; u < kBatch; ++u) z.m[u] = 0;
+    for (int64_t p0 = ps; p0 < pe; p0 += kBatch) {
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) z.m[u] = p0 + u < pe ? s_mark[p0 + u - P0] : 0;
+      sk.consume(z);
+    }
     tail_row = sk.finish();
   } else {
     // Two batches of kBatch dense rows in flight: the loads of batch k+1 are
@@ -303,6 +314,7 @@ __global__ __launch_bounds__(kWgThreads) void gather_tiles(
     Stream<T, I> st;
     st.s_col = s_col;
     st.s_val = s_val;
+    st.s_mark = s_mark;
     st.dense = dense;
     st.K = K;
     st.N = N;
@@ -313,9 +325,9 @@ __global__ __launch_bounds__(kWgThreads) void gather_tiles(
     st.issue(ba, ps);
     for (int64_t p0 = ps; p0 < pe; p0 += 2 * kBatch) {
       st.issue(bb, p0 + kBatch);
-      sk.consume(ba, p0);
+      sk.consume(ba);
       st.issue(ba, p0 + 2 * kBatch);
-      sk.consume(bb, p0 + kBatch);
+      sk.consume(bb);
     }
     tail_row = sk.finish();
   }
@@ -351,7 +363,7 @@ __global__ __launch_bounds__(kWgThreads) void gather_post(Geometry<I> g, int64_t
 #pragma unroll
     for (int i = 0; i < V; ++i) acc[i] = src[i];
     // Head partials of ranges j+1 .. k_end-1, read 8 at a time, added in order.
-    int64_t k_end = (stop + kGatherRange - 1) / kGatherRange;
+    int64_t k_end = (stop + g.range - 1) / g.range;
     if (k_end > g.nranges) k_end = g.nranges;
     constexpr int kFix = 8;
     for (int64_t k0 = j + 1; k0 < k_end; k0 += kFix) {
@@ -417,7 +429,8 @@ spmm_status gather_typed(const void* rowptr, const void* col, const void* value,
   g.row_hi = row_hi;
   g.vrows = vrows;
   g.nnz = nnz < 0 ? 0 : nnz;
-  g.nranges = g.nnz > 0 ? ceil_div(g.nnz, kGatherRange) : 1;
+  g.range = gather_range(g.nnz);
+  g.nranges = g.nnz > 0 ? ceil_div(g.nnz, g.range) : 1;
   g.Crowptr = static_cast<const I*>(Crowptr);
   g.cwin = Crowptr ? cwin : 0;
   g.climit = climit;
@@ -428,9 +441,8 @@ spmm_status gather_typed(const void* rowptr, const void* col, const void* value,
   while ((1 << log2L) < lanes_needed && log2L < 6) ++log2L;
   const int L = 1 << log2L;
   const int64_t chunks = ceil_div(lanes_needed, L);
-  // A tile stages at most kTilePositions nonzeros (LDS <= 64 KB).
   int64_t ranges_per_tile = (kWgThreads / L) / chunks;
-  if (ranges_per_tile * kGatherRange > kTilePositions) ranges_per_tile = kTilePositions / kGatherRange;
+  if (ranges_per_tile > kTileRanges) ranges_per_tile = kTileRanges;
   if (ranges_per_tile < 1) ranges_per_tile = 1;
   const int64_t groups_per_wg = ranges_per_tile * chunks;
   const int64_t wg_threads = groups_per_wg * L;
@@ -447,7 +459,7 @@ spmm_status gather_typed(const void* rowptr, const void* col, const void* value,
 
   if (g.nnz > 0) {
     const int64_t tiles = ceil_div(g.nranges, ranges_per_tile);
-    const size_t lds = static_cast<size_t>(ranges_per_tile * kGatherRange) *
+    const size_t lds = static_cast<size_t>(ranges_per_tile * g.range) *
                        (sizeof(I) + sizeof(T) + sizeof(int32_t));
     hipLaunchKernelGGL((gather_tiles<T, I>), dim3(static_cast<unsigned>(tiles)),
                        dim3(static_cast<unsigned>(wg_threads)), lds, stream, g,
@@ -468,7 +480,7 @@ spmm_status gather_typed(const void* rowptr, const void* col, const void* value,
 }  // namespace
 
 size_t gather_workspace_bytes(int64_t nnz, int64_t width) {
-  const int64_t nr = (nnz > 0 ? ceil_div(nnz, kGatherRange) : 1);
+  const int64_t nr = (nnz > 0 ? ceil_div(nnz, gather_range(nnz)) : 1);
   return align_up(static_cast<size_t>(nr) * sizeof(int64_t), 256) +
          static_cast<size_t>(2 * nr) * gather_slot_floats(width) * sizeof(float);
 }

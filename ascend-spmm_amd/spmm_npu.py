@@ -34,6 +34,26 @@ from custom_ops_lib import (  # noqa: E402
 )
 
 
+def make_start(pointer, cores):
+    """Per-core start row (or window) of an even split of ``pointer[-1]``
+    work items over ``cores``: ``searchsorted(pointer, k*ceil(total/cores),
+    right=True) - 1`` clamped at 0, as int32 (the reference's test helper,
+    tests/task_mapping/common.py:119-127).
+
+    The HIP kernels partition work on the device and do not read ``start``;
+    the operators accept it for interface compatibility and check its rank.
+    Returns a CPU tensor.
+    """
+    p = torch.as_tensor(pointer).detach().to("cpu", torch.int64).reshape(-1)
+    total = int(p[-1].item()) if p.numel() else 0
+    if total <= 0:
+        return torch.zeros(cores, dtype=torch.int32)
+    step = -(-total // cores)
+    keys = torch.arange(cores, dtype=torch.int64) * step
+    idx = torch.searchsorted(p, keys, right=True) - 1
+    return idx.clamp_min(0).to(torch.int32)
+
+
 def pack_node_tensor(tensor, inv_permutation, packed_rows=None):
     """Apply ``P`` once to a tensor whose leading dimension is original node id.
 
@@ -81,6 +101,7 @@ __all__ = [
     "block_level_split",
     "csr_to_ascend_cube",
     "csr_to_bcsr",
+    "make_start",
     "pack_node_tensor",
     "preprocess",
     "restore_node_tensor",

@@ -6,7 +6,18 @@ N=128 fp16, fp32 accumulate) — the configuration the headline metric
 A step is one SpMM call over resident device inputs.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 2] [--width N]
-                       [--op csr|mixed-empty] [--no-cpu]
+                       [--op csr|mixed|mixed-empty|graph] [--no-cpu] [--no-block-path]
+       python bench.py --copy-calibration
+
+``--op mixed`` times ``spmm_ascend_cube`` on the output of the GPU
+``preprocess`` (block windows on MFMA, the rest on the gather path); ``--op
+graph`` times pack_node_tensor -> spmm_ascend_cube on P A P^T ->
+restore_node_tensor (``preprocess(graph_layout=True)``).  Unless
+``--no-block-path`` is given, the line also carries ``block_path``: config 3
+(block-banded) at N=128 fp16, ``spmm_ascend_cube`` against ``spmm_csr`` on the
+same matrix.  ``--copy-calibration`` runs a plain 256 MiB device copy five
+times, the reference kernel for scaling the FETCH_SIZE / WRITE_SIZE counters,
+and prints the copy bandwidth.
 
 Only one GPU is used; --gpus > 1 exits with a message.
 """
@@ -30,10 +41,34 @@ import workloads  # noqa: E402
 
 METRIC = "SpMM GFLOP/s (2·nnz·N/t) and HBM GB/s % of peak, N=128 fp16, 1 MI355X"
 HBM_PEAK_GBPS = 8000.0
+MFMA_PEAK_TFLOPS = {"fp16": 2500.0, "fp32": 157.3}
+
+# HBM-side traffic per call of the dominant op, from rocprofv3 --pmc runs of
+# this script (FETCH_SIZE and WRITE_SIZE, KiB per dispatch, summed over the
+# op's kernels), scaled by what the same counters read for a plain 256 MiB
+# device copy (--copy-calibration: FETCH_SIZE reads 0.5 x the bytes copied,
+# WRITE_SIZE 1.0 x).  Keyed by (config, op, width); the counter files are
+# summarised in profiles/gather_c2_n128_pmc.md.
+FETCH_SCALE = 2.0
+WRITE_SCALE = 1.0
+PMC_KIB = {
+    (2, "csr", 128): {"fetch_kib": 205761.7 + 2951.8, "write_kib": 29334.3 + 813.2},
+}
 
 
 def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
+
+
+def host_cpu() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def cpu_baseline(w, B: np.ndarray, budget_s: float) -> dict:
@@ -61,8 +96,94 @@ def cpu_baseline(w, B: np.ndarray, budget_s: float) -> dict:
         "kind": "port",
         "sample": (f"full {w.name} matrix ({w.nnz} nnz) x N={width}, torch.sparse.mm fp32 "
                    f"(the reference's cpu_reference), median of {len(times)} reps, "
-                   f"{t * 1e3:.1f} ms/rep, os.cpu_count()={os.cpu_count()}"),
+                   f"{t * 1e3:.1f} ms/rep, torch threads {threads}, os.cpu_count()={os.cpu_count()}, "
+                   f"{host_cpu()}"),
     }
+
+
+def time_calls(step, steps: int, warmup: int, cold: bool = False):
+    """Wall ms per step over `steps` back-to-back calls (synchronised on both
+    sides) and the mean HIP-event ms per call, events recorded on the stream
+    the ops launch on (torch's current stream).  With cold=True, a 512 MiB
+    scratch write runs between calls to evict L2 and the Infinity Cache, and
+    only the events count."""
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(steps)]
+    scratch = torch.empty(512 * 1024 * 1024, dtype=torch.uint8, device="cuda") if cold else None
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        if scratch is not None:
+            scratch.fill_(i & 0xFF)
+        ev[i][0].record(stream)
+        step()
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    event_ms = float(np.mean([a.elapsed_time(b) for a, b in ev]))
+    return wall_ms, event_ms
+
+
+def device_csr(w, dev):
+    return (torch.from_numpy(w.crow.astype(np.int32)).to(dev),
+            torch.from_numpy(w.col.astype(np.int32)).to(dev),
+            torch.from_numpy(w.values).to(dev))
+
+
+def mixed_operands(spmm_npu, w, dev, graph_layout: bool):
+    """GPU preprocess of the workload; returns the spmm_ascend_cube operands
+    (without dense) and the preprocessing dict.  Not timed."""
+    crow, col, val = device_csr(w, dev)
+    p = spmm_npu.preprocess(crow, col, val, w.rows, w.cols, 16, graph_layout)
+    i32 = torch.int32
+    ccol = p["renumbered_unique_col_ids"] if graph_layout else p["unique_col_ids"]
+    vcol = p["renumbered_vcol_indices"] if graph_layout else p["vcol_indices"]
+    cstart = spmm_npu.make_start(p["crow_window_ptr"], 20).to(dev)
+    vstart = spmm_npu.make_start(p["vrow_window_ptr"], 40).to(dev)
+    ops = (p["crow_window_ptr"].to(i32), ccol.to(i32), p["value"],
+           p["vrow_window_ptr"].to(i32), vcol.to(i32), p["vvalue"])
+    return ops, cstart, vstart, p
+
+
+def block_path(spmm_npu, dev, steps: int, warmup: int) -> dict:
+    """Config 3 (block-banded) at N=128 fp16: spmm_ascend_cube after the GPU
+    preprocess against spmm_csr on the same matrix."""
+    w = workloads.make(3)
+    width = 128
+    dense = torch.from_numpy(w.dense(width)).to(dev)
+    crow, col, val = device_csr(w, dev)
+    start = spmm_npu.make_start(crow, 40).to(dev)
+    ops, cstart, vstart, p = mixed_operands(spmm_npu, w, dev, False)
+    _, csr_ms = time_calls(lambda: spmm_npu.spmm_csr(crow, col, val, dense, start), steps, warmup)
+    _, mixed_ms = time_calls(lambda: spmm_npu.spmm_ascend_cube(*ops, dense, cstart, vstart), steps, warmup)
+    nblk = int(p["crow_window_ptr"][-1].item())
+    mfma_tflops = 2.0 * 16 * nblk * width / (mixed_ms / 1e3) / 1e12
+    return {
+        "workload": f"{w.name} {w.rows}x{w.cols} nnz={w.nnz} N={width} fp16",
+        "spmm_csr_ms": round(csr_ms, 5),
+        "spmm_ascend_cube_ms": round(mixed_ms, 5),
+        "speedup_vs_spmm_csr": round(csr_ms / mixed_ms, 3),
+        "gflops": round(2.0 * w.nnz * width / (mixed_ms / 1e3) / 1e9, 1),
+        "aic_windows": int(p["crow_window_ptr"].numel() - 1),
+        "aic_blocks_16x1": nblk,
+        "vector_nnz": int(p["vvalue"].numel()),
+        "mfma_executed_tflops": round(mfma_tflops, 2),
+        "mfma_utilisation": round(mfma_tflops / MFMA_PEAK_TFLOPS["fp16"], 4),
+    }
+
+
+def copy_calibration() -> int:
+    n = 256 * 1024 * 1024
+    src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    _, ms = time_calls(lambda: dst.copy_(src), 5, 0)
+    print(json.dumps({"copy_bytes": n, "copies": 5, "ms_per_copy": round(ms, 4),
+                      "copy_gbps_read_plus_write": round(2 * n / (ms / 1e3) / 1e9, 1)}), flush=True)
+    return 0
 
 
 def main() -> int:
@@ -72,9 +193,11 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", type=int, default=2)
     ap.add_argument("--width", type=int, default=None)
-    ap.add_argument("--op", choices=["csr", "mixed-empty"], default="csr")
+    ap.add_argument("--op", choices=["csr", "mixed", "mixed-empty", "graph"], default="csr")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-block-path", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
+    ap.add_argument("--copy-calibration", action="store_true")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -83,6 +206,8 @@ def main() -> int:
               "operand is replicated, so N GPUs is N independent runs of this benchmark.",
               file=sys.stderr)
         return 2
+    if args.copy_calibration:
+        return copy_calibration()
 
     import spmm_npu
 
@@ -92,49 +217,59 @@ def main() -> int:
     log(f"[bench] workload {w.name}: {w.rows}x{w.cols}, nnz={w.nnz}, N={width}, {w.dtype}")
 
     dev = torch.device("cuda:0")
-    crow = torch.from_numpy(w.crow.astype(np.int32)).to(dev)
-    col = torch.from_numpy(w.col.astype(np.int32)).to(dev)
-    val = torch.from_numpy(w.values).to(dev)
     dense = torch.from_numpy(B).to(dev)
-    start = torch.zeros(40, dtype=torch.int32, device=dev)
+    alg_bytes = workloads.algorithmic_bytes(w, width)
     if args.op == "csr":
+        crow, col, val = device_csr(w, dev)
+        start = spmm_npu.make_start(crow, 40).to(dev)
+
         def step():
             return spmm_npu.spmm_csr(crow, col, val, dense, start)
         op_name = "spmm_csr"
-    else:
+    elif args.op == "mixed-empty":
+        crow, col, val = device_csr(w, dev)
         e_i = torch.zeros(0, dtype=torch.int32, device=dev)
         e_v = torch.zeros(0, dtype=val.dtype, device=dev)
         z1 = torch.zeros(1, dtype=torch.int32, device=dev)
         z20 = torch.zeros(20, dtype=torch.int32, device=dev)
+        start = spmm_npu.make_start(crow, 40).to(dev)
 
         def step():
             return spmm_npu.spmm_ascend_cube(z1, e_i, e_v, crow, col, val, dense, z20, start)
         op_name = "spmm_ascend_cube(vector part only)"
+    elif args.op == "mixed":
+        ops, cstart, vstart, _ = mixed_operands(spmm_npu, w, dev, False)
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    log(f"[bench] warmup {args.warmup} done")
+        def step():
+            return spmm_npu.spmm_ascend_cube(*ops, dense, cstart, vstart)
+        op_name = "preprocess -> spmm_ascend_cube (preprocess untimed)"
+    else:
+        ops, cstart, vstart, p = mixed_operands(spmm_npu, w, dev, True)
+        inv = p["inv_permutation"]
+        packed_rows = int(p["packed_rows"][0].item())
 
-    stream = torch.cuda.current_stream()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(args.steps)]
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        ev[i][0].record(stream)
-        step()
-        ev[i][1].record(stream)
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    wall_ms = (t1 - t0) * 1e3 / args.steps
-    launch_ms = float(np.mean([a.elapsed_time(b) for a, b in ev]))
-    log(f"[bench] timed {args.steps} steps: wall {wall_ms:.4f} ms/step, events {launch_ms:.4f} ms/call")
+        def step():
+            packed = spmm_npu.pack_node_tensor(dense, inv, packed_rows)
+            out = spmm_npu.spmm_ascend_cube(*ops, packed, cstart, vstart)
+            return spmm_npu.restore_node_tensor(out, inv)
+        op_name = "pack_node_tensor -> spmm_ascend_cube(P A P^T) -> restore_node_tensor"
+        s = 2 if w.dtype == "fp16" else 4
+        alg_bytes += 2 * s * w.cols * width + 2 * s * w.rows * width + 2 * 8 * w.rows
+
+    log(f"[bench] {op_name}: warmup {args.warmup}, steps {args.steps}")
+    wall_ms, event_ms = time_calls(step, args.steps, args.warmup)
+    log(f"[bench] wall {wall_ms:.4f} ms/step, events {event_ms:.4f} ms/call")
+    _, cold_ms = time_calls(step, min(args.steps, 10), 1, cold=True)
+    log(f"[bench] cold-cache events {cold_ms:.4f} ms/call")
 
     flops = 2.0 * w.nnz * width
-    alg_bytes = workloads.algorithmic_bytes(w, width)
     t_s = wall_ms / 1e3
-    achieved = alg_bytes / (launch_ms / 1e3) / 1e9
+    achieved = alg_bytes / (event_ms / 1e3) / 1e9
+    pmc = PMC_KIB.get((args.config, args.op, width))
+    traffic = None
+    if pmc is not None:
+        traffic = int(1024 * (pmc["fetch_kib"] * FETCH_SCALE + pmc["write_kib"] * WRITE_SCALE))
+    s_b = 2 if w.dtype == "fp16" else 4
     result = {
         "metric": METRIC,
         "value": round(flops / t_s / 1e9, 3),
@@ -155,17 +290,22 @@ def main() -> int:
             "index": "int32",
         },
         "hbm_gbps_algorithmic": round(alg_bytes / t_s / 1e9, 1),
+        "cold_cache_ms_per_call": round(cold_ms, 5),
         "roofline": {
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "traffic": None,
-            "algorithmic_bytes_per_launch": alg_bytes,
-            "launch_ms": round(launch_ms, 5),
+            "traffic": traffic,
+            "algorithmic_bytes_per_call": alg_bytes,
+            "gather_model_bytes": int(w.nnz * width * s_b),
+            "event_ms_per_call": round(event_ms, 5),
         },
     }
+    if not args.no_block_path and args.config == 2 and args.op == "csr":
+        log("[bench] block path (config 3, N=128) ...")
+        result["block_path"] = block_path(spmm_npu, dev, 20, 5)
     if not args.no_cpu:
         log("[bench] CPU baseline ...")
         result["cpu_baseline"] = cpu_baseline(w, B, args.cpu_budget)
