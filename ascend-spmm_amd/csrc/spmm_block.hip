@@ -16,8 +16,12 @@
 //    (j = 0..3) takes element j of each load, so its B column q is the dense
 //    column n0 + 4q + j.  Four MFMAs therefore cover a 64-column group and
 //    the accumulator lane holds 4 consecutive output columns.
-//  * The A fragment A[r][k] = Cvalue[16*(b0+k) + r] is read straight from the
-//    [block][row] layout the reference's converters produce.
+//  * A work-group first stages its chunk's block columns and values in LDS
+//    (coalesced 16-byte loads); the A fragment A[r][k] = Cvalue[16*(b0+k) + r]
+//    is then read from LDS in the [block][row] layout the reference's
+//    converters produce.  The dense rows of the next K-step are loaded while
+//    the current one is multiplied, and the accumulators are finished (plus
+//    the vector sums, rounded once) straight from registers.
 //  * Waves of the work-group take 64-column groups round-robin; each group
 //    runs the whole K loop, so every output element sees the same MFMA
 //    sequence for every width N.
@@ -49,88 +53,9 @@ typedef float float4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kXcds = 8;
 
-template <typename I>
-__device__ inline void window_group_f16(float* __restrict__ tile, const I* __restrict__ Ccol,
-                                        const _Float16* __restrict__ Cvalue, int64_t b0,
-                                        int64_t b1, const _Float16* __restrict__ dense,
-                                        int64_t K, int64_t N, int64_t n0, int lane) {
-  const int q = lane & 15, kg = lane >> 4;
-  const bool col_ok = (n0 + 4 * q) < N;
-  float4_t acc[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) acc[j] = float4_t{0.f, 0.f, 0.f, 0.f};
-
-  for (int64_t k0 = b0; k0 < b1; k0 += 32) {
-    half8_t a;
-    half4_t rows[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int64_t blk = k0 + 8 * kg + e;
-      const bool in = blk < b1;
-      a[e] = in ? Cvalue[blk * 16 + q] : static_cast<_Float16>(0.f);
-      const int64_t c = in ? static_cast<int64_t>(Ccol[blk]) : -1;
-      if (col_ok && static_cast<uint64_t>(c) < static_cast<uint64_t>(K))
-        rows[e] = *reinterpret_cast<const half4_t*>(dense + c * N + n0 + 4 * q);
-      else
-        rows[e] = half4_t{0, 0, 0, 0};
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      half8_t b;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) b[e] = rows[e][j];
-      acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[j], 0, 0, 0);
-    }
-  }
-  if (col_ok) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      float4_t v = float4_t{acc[0][e], acc[1][e], acc[2][e], acc[3][e]};
-      *reinterpret_cast<float4_t*>(tile + (4 * kg + e) * N + n0 + 4 * q) = v;
-    }
-  }
-}
-
-template <typename I>
-__device__ inline void window_group_f32(float* __restrict__ tile, const I* __restrict__ Ccol,
-                                        const float* __restrict__ Cvalue, int64_t b0,
-                                        int64_t b1, const float* __restrict__ dense, int64_t K,
-                                        int64_t N, int64_t n0, int lane) {
-  const int q = lane & 15, kg = lane >> 4;
-  const bool col_ok = (n0 + 4 * q) < N;
-  float4_t acc[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) acc[j] = float4_t{0.f, 0.f, 0.f, 0.f};
-
-  for (int64_t k0 = b0; k0 < b1; k0 += 16) {
-    float a[4];
-    float4_t bv[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int64_t blk = k0 + 4 * u + kg;
-      const bool in = blk < b1;
-      a[u] = in ? Cvalue[blk * 16 + q] : 0.f;
-      const int64_t c = in ? static_cast<int64_t>(Ccol[blk]) : -1;
-      if (col_ok && static_cast<uint64_t>(c) < static_cast<uint64_t>(K))
-        bv[u] = *reinterpret_cast<const float4_t*>(dense + c * N + n0 + 4 * q);
-      else
-        bv[u] = float4_t{0.f, 0.f, 0.f, 0.f};
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u], bv[u][j], acc[j], 0, 0, 0);
-    }
-  }
-  if (col_ok) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      float4_t v = float4_t{acc[0][e], acc[1][e], acc[2][e], acc[3][e]};
-      *reinterpret_cast<float4_t*>(tile + (4 * kg + e) * N + n0 + 4 * q) = v;
-    }
-  }
-}
+#ifndef SPMM_BLOCK_PIPELINE
+#define SPMM_BLOCK_PIPELINE 0
+#endif
 
 // Arguments shared by the block kernels.
 template <typename T, typename I>
@@ -147,6 +72,7 @@ struct BlockArgs {
   const float* vpart;      // [16*windows][N] fp32 vector sums of block-window rows (gather pass)
   float* slots;            // [noverflow][2][16][N] fp32 partials of windows longer than kbig
   int64_t kbig, noverflow, per_xcd;
+  int64_t stage;           // blocks staged in LDS at a time (multiple of the K-step)
 
   __device__ inline int64_t crp(int64_t s) const { return clampi(static_cast<int64_t>(Crowptr[s]), 0, limit); }
   __device__ inline int64_t vrp(int64_t r) const {
@@ -156,32 +82,225 @@ struct BlockArgs {
   __device__ inline bool row_has_vector(int64_t r) const { return r < vrows && vrp(r) != vrp(r + 1); }
 };
 
-// Fills the LDS tile with the MFMA sum of blocks [b0, b1) of window s.
+// LDS staging of one chunk of blocks [b0, b1) (b1 - b0 <= kbig): the block
+// columns and the 16 values of every block, loaded with coalesced 16-byte
+// pieces (Cvalue is 16-byte aligned by contract).  With `finish` set it also
+// returns the window's vector-row bits (bit r: row 16*s + r has vector-part
+// nonzeros, whose fp32 sum is in vpart), read in the same round trip.
 template <typename T, typename I>
-__device__ inline void window_tile(const BlockArgs<T, I>& a, float* tile, int64_t b0, int64_t b1) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int waves = blockDim.x >> 6;
-  const int64_t groups = (a.N + 63) / 64;
-  for (int64_t g = wave; g < groups; g += waves) {
-    if constexpr (sizeof(T) == 2)
-      window_group_f16<I>(tile, a.Ccol, a.Cvalue, b0, b1, a.dense, a.K, a.N, 64 * g, lane);
-    else
-      window_group_f32<I>(tile, a.Ccol, a.Cvalue, b0, b1, a.dense, a.K, a.N, 64 * g, lane);
+__device__ inline unsigned stage_chunk(const BlockArgs<T, I>& a, int64_t s, bool finish, int64_t b0,
+                                       int64_t b1, I* s_col, T* s_val) {
+  __shared__ unsigned s_vec;
+  const int64_t n = b1 - b0;
+  if (threadIdx.x == 0) s_vec = 0;
+  const bool vec = finish && threadIdx.x < 16 && a.row_has_vector(16 * s + threadIdx.x);
+  for (int64_t i = threadIdx.x; i < n; i += blockDim.x) s_col[i] = a.Ccol[b0 + i];
+  constexpr int64_t kPer = 16 * sizeof(T) / 16;  // 16-byte pieces per block
+  const lanes::raw16_t* src = reinterpret_cast<const lanes::raw16_t*>(a.Cvalue + 16 * b0);
+  lanes::raw16_t* dst = reinterpret_cast<lanes::raw16_t*>(s_val);
+  for (int64_t i = threadIdx.x; i < n * kPer; i += blockDim.x) dst[i] = src[i];
+  __syncthreads();
+  if (vec) atomicOr(&s_vec, 1u << threadIdx.x);
+  __syncthreads();
+  return s_vec;
+}
+
+// One K-step of dense rows per lane, loaded before the step is multiplied.
+// Lanes of blocks past the chunk end or with an invalid column get zeros
+// (never a load), so padding contributes exactly nothing.
+template <typename T> struct StepRows;
+template <> struct StepRows<_Float16> {  // 8 blocks x 4 columns per lane (K-step 32)
+  half4_t r[8];
+};
+template <> struct StepRows<float> {  // 4 blocks x 4 columns per lane (K-step 16)
+  float4_t r[4];
+};
+
+// MFMA sum of staged blocks [0, n) for the 64-column group at n0.  Lane
+// (q = lane % 16, kg = lane / 16) loads columns n0+4q .. n0+4q+3 of its
+// blocks' dense rows; MFMA j uses element j, so the accumulator lane holds 4
+// consecutive output columns (rows 4kg .. 4kg+3).  Dense loads run one K-step
+// ahead of the MFMAs.  Adds to `acc`.
+template <typename T, typename I>
+__device__ inline void group_sum(const BlockArgs<T, I>& a, const I* s_col, const T* s_val, int64_t n,
+                                 int64_t n0, int lane, float4_t (&acc)[4]) {
+  const int q = lane & 15, kg = lane >> 4;
+  const bool col_ok = (n0 + 4 * q) < a.N;
+  const int64_t coff = n0 + 4 * q;
+  if (a.K <= 0 || n <= 0) return;  // uniform: no valid dense row
+  if constexpr (sizeof(T) == 2) {
+    constexpr int64_t kStep = 32;
+    auto issue = [&](StepRows<_Float16>& st, int64_t k0) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int64_t blk = k0 + 8 * kg + e;
+        const int64_t c = blk < n ? static_cast<int64_t>(s_col[blk]) : -1;
+        if (col_ok && static_cast<uint64_t>(c) < static_cast<uint64_t>(a.K))
+          st.r[e] = *reinterpret_cast<const half4_t*>(a.dense + c * a.N + coff);
+        else
+          st.r[e] = half4_t{0, 0, 0, 0};
+      }
+    };
+    auto multiply = [&](const StepRows<_Float16>& st, int64_t k0) {
+      half8_t av;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int64_t blk = k0 + 8 * kg + e;
+        av[e] = blk < n ? s_val[blk * 16 + q] : static_cast<_Float16>(0.f);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        half8_t b;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) b[e] = st.r[e][j];
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b, acc[j], 0, 0, 0);
+      }
+    };
+#if SPMM_BLOCK_PIPELINE
+    StepRows<_Float16> sa, sb;
+    issue(sa, 0);
+    for (int64_t k0 = 0; k0 < n; k0 += 2 * kStep) {
+      const bool more = k0 + kStep < n;
+      if (more) issue(sb, k0 + kStep);
+      multiply(sa, k0);
+      if (!more) break;
+      if (k0 + 2 * kStep < n) issue(sa, k0 + 2 * kStep);
+      multiply(sb, k0 + kStep);
+    }
+#else
+    for (int64_t k0 = 0; k0 < n; k0 += kStep) {
+      StepRows<_Float16> sa;
+      issue(sa, k0);
+      multiply(sa, k0);
+    }
+#endif
+  } else {
+    constexpr int64_t kStep = 16;
+    auto issue = [&](StepRows<float>& st, int64_t k0) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int64_t blk = k0 + 4 * u + kg;
+        const int64_t c = blk < n ? static_cast<int64_t>(s_col[blk]) : -1;
+        if (col_ok && static_cast<uint64_t>(c) < static_cast<uint64_t>(a.K))
+          st.r[u] = *reinterpret_cast<const float4_t*>(a.dense + c * a.N + coff);
+        else
+          st.r[u] = float4_t{0.f, 0.f, 0.f, 0.f};
+      }
+    };
+    auto multiply = [&](const StepRows<float>& st, int64_t k0) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int64_t blk = k0 + 4 * u + kg;
+        const float av = blk < n ? s_val[blk * 16 + q] : 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, st.r[u][j], acc[j], 0, 0, 0);
+      }
+    };
+#if SPMM_BLOCK_PIPELINE
+    StepRows<float> sa, sb;
+    issue(sa, 0);
+    for (int64_t k0 = 0; k0 < n; k0 += 2 * kStep) {
+      const bool more = k0 + kStep < n;
+      if (more) issue(sb, k0 + kStep);
+      multiply(sa, k0);
+      if (!more) break;
+      if (k0 + 2 * kStep < n) issue(sa, k0 + 2 * kStep);
+      multiply(sb, k0 + kStep);
+    }
+#else
+    for (int64_t k0 = 0; k0 < n; k0 += kStep) {
+      StepRows<float> sa;
+      issue(sa, k0);
+      multiply(sa, k0);
+    }
+#endif
   }
 }
 
-// Finishes window s from its fp32 block sum (LDS tile or `src`): adds the
-// vector sums of rows that have them (block first, then vector part), rounds
-// once and writes rows 16*s .. 16*s+15.
+// Bit r set: row 16*s + r has vector-part nonzeros (their fp32 sum is in
+// vpart).  All threads of the work-group must call it.
 template <typename T, typename I>
-__device__ inline void finish_window(const BlockArgs<T, I>& a, int64_t s, const float* src) {
-  constexpr int V = LaneVec<T>::V;
-  __shared__ unsigned s_vec;  // bit r: row 16*s + r has vector nonzeros
+__device__ inline unsigned window_vector_rows(const BlockArgs<T, I>& a, int64_t s) {
+  __shared__ unsigned s_vec;
   if (threadIdx.x == 0) s_vec = 0;
   __syncthreads();
   if (threadIdx.x < 16 && a.row_has_vector(16 * s + threadIdx.x)) atomicOr(&s_vec, 1u << threadIdx.x);
   __syncthreads();
-  const unsigned vec = s_vec;
+  return s_vec;
+}
+
+// Sums blocks [b0, b1) of window s and, with `slot` null, finishes rows
+// 16*s .. 16*s+15 straight from the accumulators: block sum, plus the row's
+// vector sum if it has one, rounded once.  With `slot` set, the fp32 block
+// sum goes to that [16][N] workspace slot instead.  Blocks are staged in LDS
+// `a.stage` at a time (a multiple of the K-step, so the MFMA sequence does
+// not depend on it); a window that fits is staged once for all column groups.
+template <typename T, typename I>
+__device__ inline void window_chunk(const BlockArgs<T, I>& a, int64_t s, int64_t b0, int64_t b1,
+                                    float* slot, I* s_col, T* s_val) {
+  const int64_t n = b1 - b0;
+  const bool once = n <= a.stage;
+  unsigned vec = 0;
+  if (once)
+    vec = stage_chunk(a, s, slot == nullptr, b0, b1, s_col, s_val);
+  else if (slot == nullptr)
+    vec = window_vector_rows(a, s);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int waves = blockDim.x >> 6;
+  const int q = lane & 15, kg = lane >> 4;
+  const int64_t groups = (a.N + 63) / 64;
+  // Uniform trip count over the work-group (staging synchronises it).
+  for (int64_t gbase = 0; gbase < groups; gbase += waves) {
+    const int64_t g = gbase + wave;
+    const bool active = g < groups;
+    const int64_t n0 = 64 * g;
+    float4_t acc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[j] = float4_t{0.f, 0.f, 0.f, 0.f};
+    if (once) {
+      if (active) group_sum(a, s_col, s_val, n, n0, lane, acc);
+    } else {
+      for (int64_t sb = 0; sb < n; sb += a.stage) {
+        const int64_t m = n - sb < a.stage ? n - sb : a.stage;
+        __syncthreads();  // the previous piece is no longer read
+        stage_chunk(a, s, false, b0 + sb, b0 + sb + m, s_col, s_val);
+        if (active) group_sum(a, s_col, s_val, m, n0, lane, acc);
+      }
+    }
+    const int64_t c0 = n0 + 4 * q;
+    if (!active || c0 >= a.N) continue;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int r = 4 * kg + e;
+      float v[4] = {acc[0][e], acc[1][e], acc[2][e], acc[3][e]};
+      if (slot) {
+        *reinterpret_cast<float4_t*>(slot + r * a.N + c0) = float4_t{v[0], v[1], v[2], v[3]};
+        continue;
+      }
+      const int64_t row = 16 * s + r;
+      if (vec >> r & 1u) {
+        const float4_t p = *reinterpret_cast<const float4_t*>(a.vpart + row * a.N + c0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = v[i] + p[i];
+      }
+      if constexpr (sizeof(T) == 2) {
+        *reinterpret_cast<half4_t*>(a.out + row * a.N + c0) =
+            half4_t{static_cast<_Float16>(v[0]), static_cast<_Float16>(v[1]),
+                    static_cast<_Float16>(v[2]), static_cast<_Float16>(v[3])};
+      } else {
+        *reinterpret_cast<float4_t*>(a.out + row * a.N + c0) = float4_t{v[0], v[1], v[2], v[3]};
+      }
+    }
+  }
+}
+
+// Finishes window s from an fp32 [16][N] sum in LDS (the combine kernel):
+// adds the vector sums of rows that have them, rounds once, writes the rows.
+template <typename T, typename I>
+__device__ inline void finish_window(const BlockArgs<T, I>& a, int64_t s, const float* src) {
+  constexpr int V = LaneVec<T>::V;
+  const unsigned vec = window_vector_rows(a, s);
   const int64_t chunks = a.N / V;
   for (int64_t it = threadIdx.x; it < 16 * chunks; it += blockDim.x) {
     const int64_t r = it / chunks;
@@ -199,11 +318,6 @@ __device__ inline void finish_window(const BlockArgs<T, I>& a, int64_t s, const 
   }
 }
 
-// Copies the 16 x N fp32 tile to a workspace slot.
-__device__ inline void save_tile(const float* tile, int64_t N, float* dst) {
-  for (int64_t i = threadIdx.x; i < 16 * N; i += blockDim.x) dst[i] = tile[i];
-}
-
 // Work-groups [0, 8*per_xcd): window s (XCD-aware order) computes its first
 // kbig blocks; a window with at most kbig blocks is finished here.  A longer
 // window leaves its first-chunk sum in slot (k0, 1), k0 = (b0 + kbig) / kbig.
@@ -211,10 +325,17 @@ __device__ inline void save_tile(const float* tile, int64_t N, float* dst) {
 // Only the window holding block k*kbig can have blocks past its first chunk
 // in that range; that segment's sum goes to slot (k, 0).
 template <typename T, typename I>
-__global__ __launch_bounds__(256) void block_windows(BlockArgs<T, I> a) {
-  extern __shared__ float tile[];  // [16][N] fp32
+#ifndef SPMM_BLOCK_WAVES
+#define SPMM_BLOCK_WAVES 4
+#endif
+// Waves per SIMD the register budget of block_windows is fitted to.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SPMM_BLOCK_WAVES))) void block_windows(BlockArgs<T, I> a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  T* s_val = reinterpret_cast<T*>(smem);                           // [stage][16]
+  I* s_col = reinterpret_cast<I*>(smem + a.stage * 16 * sizeof(T));  // [stage]
   const int64_t lead = a.per_xcd * kXcds;
   const int64_t g = blockIdx.x;
+  const int64_t n16 = 16 * a.N;
   if (g < lead) {
     const int64_t s = (g % kXcds) * a.per_xcd + g / kXcds;
     if (s >= a.windows) return;  // uniform over the work-group
@@ -223,12 +344,8 @@ __global__ __launch_bounds__(256) void block_windows(BlockArgs<T, I> a) {
     if (b1 <= b0) return;  // empty window: rows handled by the vector pass
     const bool single = b1 - b0 <= a.kbig;
     if (!single) b1 = b0 + a.kbig;
-    window_tile(a, tile, b0, b1);
-    __syncthreads();
-    if (single)
-      finish_window(a, s, tile);
-    else
-      save_tile(tile, a.N, a.slots + (2 * ((b0 + a.kbig) / a.kbig) + 1) * 16 * a.N);
+    window_chunk(a, s, b0, b1, single ? nullptr : a.slots + (2 * ((b0 + a.kbig) / a.kbig) + 1) * n16,
+                 s_col, s_val);
     return;
   }
   const int64_t k = g - lead;
@@ -244,9 +361,7 @@ __global__ __launch_bounds__(256) void block_windows(BlockArgs<T, I> a) {
   const int64_t lo = b0 + a.kbig > bk ? b0 + a.kbig : bk;
   const int64_t hi = b1 < bk + a.kbig ? b1 : bk + a.kbig;
   if (lo >= hi) return;
-  window_tile(a, tile, lo, hi);
-  __syncthreads();
-  save_tile(tile, a.N, a.slots + (2 * k) * 16 * a.N);
+  window_chunk(a, s, lo, hi, a.slots + (2 * k) * n16, s_col, s_val);
 }
 
 // Work-group k: if a window's blocks past its first chunk start in overflow
@@ -301,14 +416,20 @@ spmm_status block_typed(const void* Crowptr, const void* Ccol, const void* Cvalu
   a.per_xcd = ceil_div(windows, kXcds);
   const int64_t groups = (N + 63) / 64;
   const int waves = groups < 4 ? static_cast<int>(groups) : 4;
-  const size_t lds = static_cast<size_t>(16) * N * sizeof(float);
+  // Staging piece: about twice the mean window, 64 .. kbig blocks, so LDS per
+  // work-group stays small for small windows and most windows stage once.
+  const int64_t mean = a.limit / windows;
+  a.stage = 64;
+  while (a.stage < 2 * mean && a.stage < a.kbig) a.stage *= 2;
+  const size_t stage_lds = static_cast<size_t>(a.stage) * (16 * sizeof(T) + sizeof(I));
   const int64_t grid = a.per_xcd * kXcds + a.noverflow;
-  hipLaunchKernelGGL((block_windows<T, I>), dim3(static_cast<unsigned>(grid)), dim3(64 * waves), lds,
-                     stream, a);
+  hipLaunchKernelGGL((block_windows<T, I>), dim3(static_cast<unsigned>(grid)), dim3(64 * waves),
+                     stage_lds, stream, a);
   if (spmm_status st = check_launch("block_windows")) return st;
   if (a.noverflow == 0) return SPMM_OK;
-  hipLaunchKernelGGL((block_combine<T, I>), dim3(static_cast<unsigned>(a.noverflow)), dim3(256), lds, stream,
-                     a);
+  const size_t tile_lds = static_cast<size_t>(16) * N * sizeof(float);
+  hipLaunchKernelGGL((block_combine<T, I>), dim3(static_cast<unsigned>(a.noverflow)), dim3(256), tile_lds,
+                     stream, a);
   return check_launch("block_combine");
 }
 

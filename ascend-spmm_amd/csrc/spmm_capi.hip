@@ -158,6 +158,8 @@ spmm_status spmm_mixed_run(const spmm_mixed_desc* d, const void* Crowptr, const 
       (d->vector_nnz > 0 && (Vcol == nullptr || Vvalue == nullptr)))
     return fail(SPMM_ERR_INVALID_ARGUMENT, "spmm_ascend_cube: null device pointer");
   if (spmm_status st = check_aligned(dense, out, "spmm_ascend_cube")) return st;
+  if (reinterpret_cast<uintptr_t>(Cvalue) % 16 != 0)
+    return fail(SPMM_ERR_CONTRACT, "spmm_ascend_cube: Cvalue must be 16-byte aligned");
   hipStream_t s = as_stream(stream);
   const MixedLayout lay(d);
   if (workspace == nullptr || workspace_bytes < lay.total())

@@ -15,11 +15,12 @@
 //    only on the positions and nnz, so every output element sees the same
 //    fp32 operation sequence for every width N: results are deterministic and
 //    bit-identical across widths.
-//  * gather_tiles: a work-group takes a tile of consecutive ranges.  It finds
-//    the rows starting in the tile with a work-group-wide many-way search of
-//    the row pointer (a few rounds of one load per thread instead of a chain
-//    of dependent loads), stages the tile's column ids and values in LDS and
-//    marks, per position, the row that starts there.  Each lane group then
+//  * gather_tile_rows (one thread per row) records, for every tile, the row
+//    holding the tile's first position.
+//  * gather_tiles: a work-group takes a tile of consecutive ranges.  It reads
+//    its row span from that table while it stages the tile's column ids and
+//    values in LDS (one round trip), then marks, per position, the row that
+//    starts there.  Each lane group then
 //    streams its range flat: the dense rows of 8 consecutive nonzeros are
 //    loaded together, two batches in flight (16 bytes per lane; the L lanes
 //    of a group read L*16 contiguous bytes of one dense row), accumulated in
@@ -31,7 +32,6 @@
 //    partials in range order.
 #include "common.h"
 #include "lanevec.h"
-#include "wgsearch.h"
 
 namespace spmm {
 namespace {
@@ -55,6 +55,7 @@ template <typename I>
 struct Geometry {
   const I* rowptr;
   int64_t* tail;           // [nranges]: row that starts in range j and runs past its end, or -1
+  int64_t* tile_row;       // [tiles + 1]: row holding the first position of tile t
   int64_t row_lo, row_hi;  // rows handled
   int64_t vrows;           // rowptr holds vrows + 1 entries; rows >= vrows are empty
   int64_t nnz;             // extent of col[] / value[]
@@ -189,7 +190,11 @@ struct Sink {
 };
 
 template <typename T, typename I>
-__global__ __launch_bounds__(kWgThreads) void gather_tiles(
+#ifndef SPMM_GATHER_WAVES
+#define SPMM_GATHER_WAVES 4
+#endif
+// Waves per SIMD the register budget of gather_tiles is fitted to.
+__global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM_GATHER_WAVES))) void gather_tiles(
     Geometry<I> g, const I* __restrict__ col, const T* __restrict__ value,
     const T* __restrict__ dense, int64_t K, int64_t N, T* __restrict__ out, float* __restrict__ ws,
     int log2L, int64_t chunks, int64_t ranges_per_tile, int64_t slot) {
@@ -203,41 +208,37 @@ __global__ __launch_bounds__(kWgThreads) void gather_tiles(
   const int64_t j0 = static_cast<int64_t>(blockIdx.x) * ranges_per_tile;
   const int64_t j1 = (j0 + ranges_per_tile < g.nranges) ? j0 + ranges_per_tile : g.nranges;
   const int64_t P0 = g.lo(j0), P1 = g.hi(j1 - 1);
-  const bool last_tile = j1 == g.nranges;
   const int64_t base = g.rp(g.row_lo), end = g.rp(g.row_hi);
 
-  // Rows overlapping the tile: [rS, rE) with rS = the last row whose end is
-  // at most P0 (first row with rp >= P0+1, minus one) and rE = the first row
-  // with rp >= P1+1.  Runs of empty rows before the tile are skipped.
-  int64_t rS, rE;
-  wg_lower_bound2([&](int64_t r) { return g.rp(r); }, g.row_lo, g.row_hi, P0 + 1, P1 + 1, rS, rE);
-  rS = rS - 1 > g.row_lo ? rS - 1 : g.row_lo;
+  // Rows overlapping the tile: [rS, rE) with rS = the row holding position P0
+  // and rE = one past the row holding P1 (the next tile's first position),
+  // from the tile-row table of gather_tile_rows; tiles starting outside our
+  // positions [base, end) clamp to the row range.  Runs of empty rows before
+  // the tile are skipped.
+  const int64_t rS = P0 < base ? g.row_lo : (P0 < end ? g.tile_row[blockIdx.x] : g.row_hi);
+  const int64_t rE = P1 < base ? g.row_lo : (P1 < end ? g.tile_row[blockIdx.x + 1] + 1 : g.row_hi);
 
-  // Stage the tile's nonzeros of our rows ([base, end)) and clear the marks;
-  // each thread issues its loads before the first LDS store.
-  const bool any = base < end && P0 < end && P1 > base;  // uniform over the work-group
+  // Stage the tile's column ids and values (positions clamped to [0, nnz);
+  // those outside our rows are never read) and clear the marks.  The loads
+  // do not wait for the row lookups above; each thread issues its loads
+  // before the first LDS store.
   for (int64_t i0 = 0; i0 < tile_positions; i0 += kStageUnroll * blockDim.x) {
     I cs[kStageUnroll];
     T vs[kStageUnroll];
-    if (any) {
 #pragma unroll
-      for (int k = 0; k < kStageUnroll; ++k) {
-        int64_t p = P0 + i0 + k * blockDim.x + threadIdx.x;
-        p = p < base ? base : (p >= end ? end - 1 : p);
-        cs[k] = col[p];
-        vs[k] = value[p];
-      }
+    for (int k = 0; k < kStageUnroll; ++k) {
+      int64_t p = P0 + i0 + k * blockDim.x + threadIdx.x;
+      p = p < g.nnz ? p : g.nnz - 1;
+      cs[k] = col[p];
+      vs[k] = value[p];
     }
 #pragma unroll
     for (int k = 0; k < kStageUnroll; ++k) {
       const int64_t i = i0 + k * blockDim.x + threadIdx.x;
-      const int64_t p = P0 + i;
       if (i < tile_positions) {
         s_mark[i] = 0;
-        if (any && p >= base && p < end) {
-          s_col[i] = cs[k];
-          s_val[i] = vs[k];
-        }
+        s_col[i] = cs[k];
+        s_val[i] = vs[k];
       }
     }
   }
@@ -332,6 +333,18 @@ __global__ __launch_bounds__(kWgThreads) void gather_tiles(
     tail_row = sk.finish();
   }
   if (reporter) g.tail[j] = tail_row;
+}
+
+// Tile-row table: for every tile t whose first position P = t*T lies in a
+// row of [row_lo, row_hi), tile_row[t] = that row.  One thread per row writes
+// the tile starts inside its nonzero span [rp(r), rp(r+1)).
+template <typename I>
+__global__ __launch_bounds__(kWgThreads) void gather_tile_rows(Geometry<I> g, int64_t T, int64_t tiles) {
+  const int64_t r = g.row_lo + static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (r >= g.row_hi) return;
+  const int64_t a = g.rp(r), b = g.rp(r + 1);
+  const int64_t t_end = (b + T - 1) / T < tiles ? (b + T - 1) / T : tiles;
+  for (int64_t t = (a + T - 1) / T; t < t_end; ++t) g.tile_row[t] = r;
 }
 
 // Post pass, one launch:
@@ -448,17 +461,22 @@ spmm_status gather_typed(const void* rowptr, const void* col, const void* value,
   const int64_t wg_threads = groups_per_wg * L;
   const int64_t slot = gather_slot_floats(N);
 
-  // Workspace: tail rows, then the partial slots (256-byte aligned).
-  const size_t tail_bytes = align_up(static_cast<size_t>(g.nranges) * sizeof(int64_t), 256);
+  // Workspace: tail rows and the tile-row table, then the partial slots
+  // (256-byte aligned).
+  const size_t tail_bytes = align_up(static_cast<size_t>(2 * g.nranges + 1) * sizeof(int64_t), 256);
   const size_t need = tail_bytes + static_cast<size_t>(2 * g.nranges) * slot * sizeof(float);
   if (ws == nullptr || ws_bytes < need)
     return fail(SPMM_ERR_CONTRACT, "gather workspace too small: need " + std::to_string(need) +
                                        " bytes, got " + std::to_string(ws_bytes));
   g.tail = static_cast<int64_t*>(ws);
+  g.tile_row = g.tail + g.nranges;
   float* partial = reinterpret_cast<float*>(static_cast<char*>(ws) + tail_bytes);
 
   if (g.nnz > 0) {
     const int64_t tiles = ceil_div(g.nranges, ranges_per_tile);
+    hipLaunchKernelGGL((gather_tile_rows<I>), dim3(static_cast<unsigned>(ceil_div(row_hi - row_lo, kWgThreads))),
+                       dim3(kWgThreads), 0, stream, g, ranges_per_tile * g.range, tiles);
+    if (spmm_status st = check_launch("gather_tile_rows")) return st;
     const size_t lds = static_cast<size_t>(ranges_per_tile * g.range) *
                        (sizeof(I) + sizeof(T) + sizeof(int32_t));
     hipLaunchKernelGGL((gather_tiles<T, I>), dim3(static_cast<unsigned>(tiles)),
@@ -481,7 +499,7 @@ spmm_status gather_typed(const void* rowptr, const void* col, const void* value,
 
 size_t gather_workspace_bytes(int64_t nnz, int64_t width) {
   const int64_t nr = (nnz > 0 ? ceil_div(nnz, gather_range(nnz)) : 1);
-  return align_up(static_cast<size_t>(nr) * sizeof(int64_t), 256) +
+  return align_up(static_cast<size_t>(2 * nr + 1) * sizeof(int64_t), 256) +
          static_cast<size_t>(2 * nr) * gather_slot_floats(width) * sizeof(float);
 }
 

@@ -83,9 +83,10 @@ void check_same_device(const at::Tensor& a, const at::Tensor& b, const char* nam
   TORCH_CHECK(a.device() == b.device(), name, " must be on the same device as dense");
 }
 
-// The kernels read dense in 16-byte pieces; a view at an odd offset is copied.
-at::Tensor aligned(const at::Tensor& dense) {
-  return reinterpret_cast<uintptr_t>(dense.data_ptr()) % 16 == 0 ? dense : dense.clone();
+// The kernels read dense and Cvalue in 16-byte pieces; a view at an offset
+// that is not a multiple of 16 bytes is copied.
+at::Tensor aligned(const at::Tensor& t) {
+  return reinterpret_cast<uintptr_t>(t.data_ptr()) % 16 == 0 ? t : t.clone();
 }
 
 at::Tensor workspace(const at::Tensor& like, size_t bytes) {
@@ -146,7 +147,7 @@ at::Tensor run_mixed(const at::Tensor& Crowptr, const at::Tensor& Ccol_ids, cons
   c10::DeviceGuard guard(dense.device());
   const at::Tensor crp = Crowptr.contiguous(), ccl = Ccol_ids.contiguous();
   const at::Tensor vrp = Vrowptr.contiguous(), vcl = Vcol_ids.contiguous();
-  const at::Tensor dn = aligned(dense);
+  const at::Tensor dn = aligned(dense), cv = aligned(Cvalue);
   spmm_mixed_desc d;
   d.block_windows = std::max<int64_t>(Crowptr.size(0) - 1, 0);
   d.block_count = Ccol_ids.size(0);
@@ -163,7 +164,7 @@ at::Tensor run_mixed(const at::Tensor& Crowptr, const at::Tensor& Ccol_ids, cons
   size_t ws_bytes = 0;
   raise_status(spmm_mixed_workspace(&d, &ws_bytes), op_name);
   at::Tensor ws = workspace(dense, ws_bytes);
-  raise_status(spmm_mixed_run(&d, crp.data_ptr(), ccl.data_ptr(), Cvalue.data_ptr(), vrp.data_ptr(),
+  raise_status(spmm_mixed_run(&d, crp.data_ptr(), ccl.data_ptr(), cv.data_ptr(), vrp.data_ptr(),
                               vcl.data_ptr(), Vvalue.data_ptr(), dn.data_ptr(), result.data_ptr(),
                               ws.data_ptr(), ws_bytes, current_stream(dense)),
                op_name);

@@ -105,11 +105,13 @@ spmm_status spmm_csr_run(const spmm_csr_desc* desc,
  * (kernels/op_kernel/spmm_ascend_cube.cpp:16-311, 543-907).  The per-core
  * Cstart/Vstart arrays of the reference are not needed.
  *
- * The block part (16x1 BCSR windows) runs on fp16/fp32 MFMA; rows of block
- * windows also take their vector-part nonzeros in the same work-group, added
- * after the block sum.  Rows at or beyond 16*block_windows take the CSR gather
- * path of spmm_csr, so with block_windows == 0 the result is bit-identical to
- * spmm_csr on the same CSR.  Every output row is written.
+ * The block part (16x1 BCSR windows) runs on fp16/fp32 MFMA.  The vector
+ * part runs the CSR gather path of spmm_csr first; for rows of block windows
+ * that have blocks it leaves the fp32 vector sum in the workspace, and the
+ * block kernel adds it after the block sum and rounds once.  With
+ * block_windows == 0 the result is bit-identical to spmm_csr on the same CSR.
+ * Every output row is written.  dense, out and Cvalue must be 16-byte
+ * aligned (SPMM_ERR_CONTRACT otherwise).
  * ---------------------------------------------------------------------- */
 typedef struct spmm_mixed_desc {
   int64_t block_windows;  /* Crowptr.numel - 1                              */
