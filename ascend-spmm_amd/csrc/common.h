@@ -38,7 +38,7 @@ inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 // to cover memory latency.  It depends on nnz only (not on width or dtype),
 // which is what makes the gather results identical for every feature width.
 #ifndef SPMM_GATHER_SPLIT
-#define SPMM_GATHER_SPLIT 24576
+#define SPMM_GATHER_SPLIT 12288
 #endif
 constexpr int64_t kGatherSplit = SPMM_GATHER_SPLIT;
 constexpr int64_t kGatherRangeMin = 16;

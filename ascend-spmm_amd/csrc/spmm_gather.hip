@@ -26,10 +26,13 @@
 //    of a group read L*16 contiguous bytes of one dense row), accumulated in
 //    order, and flushed wherever the next position starts a new row.  Empty
 //    rows are written as zeros.
-//  * A row that crosses range ends leaves one fp32 partial per range in the
-//    workspace ("tail" in the range where it starts, "head" in every later
-//    range) and its id in the range's tail entry; gather_fixup adds the
-//    partials in range order.
+//  * A short row (at most R/2 nonzeros) is summed entirely by the lane group
+//    of the range where it starts (running on into the next range, staged as
+//    a halo); the next range skips it.  So every such row is one
+//    sequential fp32 sum, and only longer rows are split: they leave one fp32
+//    partial per range in the workspace ("tail" in the range where they
+//    start, "head" in every later range) and their id in the range's tail
+//    entry; the post pass adds the partials in range order.
 #include "common.h"
 #include "lanevec.h"
 
@@ -45,6 +48,11 @@ constexpr int kWgThreads = 256;
 #endif
 constexpr int kBatch = SPMM_GATHER_BATCH;  // dense rows per batch (two batches in flight)
 constexpr int kStageUnroll = 8;             // staging loads issued per thread before storing
+// A row is "short" (summed by one lane group, never split) when it holds at
+// most R / SPMM_GATHER_SHORT_DIV nonzeros.
+#ifndef SPMM_GATHER_SHORT_DIV
+#define SPMM_GATHER_SHORT_DIV 2
+#endif
 #ifndef SPMM_GATHER_TILE_RANGES
 #define SPMM_GATHER_TILE_RANGES 16
 #endif
@@ -200,10 +208,15 @@ __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM
     int log2L, int64_t chunks, int64_t ranges_per_tile, int64_t slot) {
   constexpr int V = LaneVec<T>::V;
   extern __shared__ __align__(16) unsigned char smem[];
-  const int64_t tile_positions = ranges_per_tile * g.range;
+  // The tile's positions plus a halo of one range: a short row that starts
+  // in the tile's last range is finished from the halo.
+  const int64_t tile_positions = (ranges_per_tile + 1) * g.range;
   I* s_col = reinterpret_cast<I*>(smem);
   T* s_val = reinterpret_cast<T*>(smem + tile_positions * sizeof(I));
   int32_t* s_mark = reinterpret_cast<int32_t*>(smem + tile_positions * (sizeof(I) + sizeof(T)));
+  // s_cut[k]: end (relative to P0) of the short row crossing the tile's k-th
+  // range boundary P0 + k*R, or -1.
+  __shared__ int32_t s_cut[kTileRanges + 1];
 
   const int64_t j0 = static_cast<int64_t>(blockIdx.x) * ranges_per_tile;
   const int64_t j1 = (j0 + ranges_per_tile < g.nranges) ? j0 + ranges_per_tile : g.nranges;
@@ -222,6 +235,8 @@ __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM
   // those outside our rows are never read) and clear the marks.  The loads
   // do not wait for the row lookups above; each thread issues its loads
   // before the first LDS store.
+  const int64_t nr = j1 - j0;
+  if (threadIdx.x <= nr) s_cut[threadIdx.x] = -1;
   for (int64_t i0 = 0; i0 < tile_positions; i0 += kStageUnroll * blockDim.x) {
     I cs[kStageUnroll];
     T vs[kStageUnroll];
@@ -243,18 +258,27 @@ __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM
     }
   }
   __syncthreads();
-  // Mark the starts and ends of the tile's non-empty rows; each position is
-  // marked only by the row that holds it.  Empty rows are left to the post pass.
+  // Mark the starts and ends of the tile's non-empty rows (ends also in the
+  // halo); each position is marked only by the row that holds it.  A short
+  // row (at most R / SPMM_GATHER_SHORT_DIV nonzeros) that crosses a range
+  // boundary is owned by the
+  // range where it starts: s_cut tells that range how far to run on and the
+  // next range where to begin.  Longer rows leave one fp32 partial per range
+  // instead.  Empty rows are left to the post pass.
   for (int64_t r = rS + threadIdx.x; r < rE; r += blockDim.x) {
     const int64_t a = g.rp(r), b = g.rp(r + 1);
     if (a < b) {
       const bool start_in = a >= P0 && a < P1 && r - rS < (INT32_MAX >> 2) - 1;
-      const bool end_in = b - 1 >= P0 && b - 1 < P1;
+      const bool end_in = b - 1 >= P0 && b - 1 < P0 + tile_positions;
       if (start_in) {
         const int32_t vp = g.in_block_window(r) ? 2 : 0;
         s_mark[a - P0] = static_cast<int32_t>((r - rS + 1) << 2) | vp | (end_in && b - 1 == a ? 1 : 0);
       }
       if (end_in && !(start_in && b - 1 == a)) s_mark[b - 1 - P0] = 1;
+      if (b - a <= g.range / SPMM_GATHER_SHORT_DIV) {
+        const int64_t k = a < P0 ? 0 : (a - P0) / g.range + 1;  // first boundary after a
+        if (k <= nr && P0 + k * g.range < b) s_cut[k] = static_cast<int32_t>(b - P0);
+      }
     }
   }
   __syncthreads();
@@ -269,8 +293,11 @@ __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM
   const bool reporter = lane == 0 && cc == 0;  // writes tail[j]
   const int64_t c0 = (cc * L + lane) * V;
   const int64_t lo = g.lo(j), hi = g.hi(j);
-  const int64_t ps = lo > base ? lo : base;
-  const int64_t pe = hi < end ? hi : end;
+  // Skip the short row owned by the previous range; run on to the end of the
+  // short row this range owns past its end.
+  const int32_t cut_in = s_cut[j - j0], cut_out = s_cut[j - j0 + 1];
+  const int64_t ps = cut_in >= 0 ? P0 + cut_in : (lo > base ? lo : base);
+  const int64_t pe = cut_out >= 0 ? P0 + cut_out : (hi < end ? hi : end);
   if (ps >= pe || c0 >= N) {
     if (reporter) g.tail[j] = -1;
     return;
@@ -477,7 +504,7 @@ spmm_status gather_typed(const void* rowptr, const void* col, const void* value,
     hipLaunchKernelGGL((gather_tile_rows<I>), dim3(static_cast<unsigned>(ceil_div(row_hi - row_lo, kWgThreads))),
                        dim3(kWgThreads), 0, stream, g, ranges_per_tile * g.range, tiles);
     if (spmm_status st = check_launch("gather_tile_rows")) return st;
-    const size_t lds = static_cast<size_t>(ranges_per_tile * g.range) *
+    const size_t lds = static_cast<size_t>((ranges_per_tile + 1) * g.range) *
                        (sizeof(I) + sizeof(T) + sizeof(int32_t));
     hipLaunchKernelGGL((gather_tiles<T, I>), dim3(static_cast<unsigned>(tiles)),
                        dim3(static_cast<unsigned>(wg_threads)), lds, stream, g,

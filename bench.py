@@ -6,7 +6,7 @@ N=128 fp16, fp32 accumulate) — the configuration the headline metric
 A step is one SpMM call over resident device inputs.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 2] [--width N]
-                       [--op csr|mixed|mixed-empty|graph] [--no-cpu] [--no-block-path]
+                       [--op csr|mixed|mixed-empty|graph] [--no-cpu] [--no-block-path] [--no-cold]
        python bench.py --copy-calibration
 
 ``--op mixed`` times ``spmm_ascend_cube`` on the output of the GPU
@@ -43,16 +43,20 @@ METRIC = "SpMM GFLOP/s (2·nnz·N/t) and HBM GB/s % of peak, N=128 fp16, 1 MI355
 HBM_PEAK_GBPS = 8000.0
 MFMA_PEAK_TFLOPS = {"fp16": 2500.0, "fp32": 157.3}
 
-# HBM-side traffic per call of the dominant op, from rocprofv3 --pmc runs of
-# this script (FETCH_SIZE and WRITE_SIZE, KiB per dispatch, summed over the
-# op's kernels), scaled by what the same counters read for a plain 256 MiB
-# device copy (--copy-calibration: FETCH_SIZE reads 0.5 x the bytes copied,
-# WRITE_SIZE 1.0 x).  Keyed by (config, op, width); the counter files are
-# summarised in profiles/gather_c2_n128_pmc.md.
+# HBM-side traffic per call of the op, from rocprofv3 --pmc runs of this
+# script (FETCH_SIZE and WRITE_SIZE, KiB per dispatch, summed over the op's
+# kernels, warm calls only: --no-cold), scaled by what the same counters read
+# for a plain 256 MiB device copy (--copy-calibration: FETCH_SIZE reads 0.5 x
+# the bytes copied, WRITE_SIZE 1.0 x).  The counters see L2-to-fabric
+# traffic, Infinity Cache hits included.  Keyed by (config, op, width); the
+# runs are summarised in profiles/*_traffic.md.  Re-measured whenever the
+# kernels change.
 FETCH_SCALE = 2.0
 WRITE_SCALE = 1.0
 PMC_KIB = {
-    (2, "csr", 128): {"fetch_kib": 205761.7 + 2951.8, "write_kib": 29334.3 + 813.2},
+    (2, "csr", 128): {"fetch_kib": 216159.0 + 3876.9 + 245.5, "write_kib": 41413.3 + 659.8 + 16.4},
+    (3, "mixed", 128): {"fetch_kib": 124684.9 + 6310.1 + 169.7 + 131811.5 + 107.0,
+                        "write_kib": 22351.1 + 2266.5 + 8.1 + 14116.0 + 0.0},
 }
 
 
@@ -198,6 +202,7 @@ def main() -> int:
     ap.add_argument("--no-block-path", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--copy-calibration", action="store_true")
+    ap.add_argument("--no-cold", action="store_true", help="skip the cold-cache timing (counter runs)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -259,8 +264,10 @@ def main() -> int:
     log(f"[bench] {op_name}: warmup {args.warmup}, steps {args.steps}")
     wall_ms, event_ms = time_calls(step, args.steps, args.warmup)
     log(f"[bench] wall {wall_ms:.4f} ms/step, events {event_ms:.4f} ms/call")
-    _, cold_ms = time_calls(step, min(args.steps, 10), 1, cold=True)
-    log(f"[bench] cold-cache events {cold_ms:.4f} ms/call")
+    cold_ms = None
+    if not args.no_cold:
+        _, cold_ms = time_calls(step, min(args.steps, 10), 1, cold=True)
+        log(f"[bench] cold-cache events {cold_ms:.4f} ms/call")
 
     flops = 2.0 * w.nnz * width
     t_s = wall_ms / 1e3
@@ -290,7 +297,7 @@ def main() -> int:
             "index": "int32",
         },
         "hbm_gbps_algorithmic": round(alg_bytes / t_s / 1e9, 1),
-        "cold_cache_ms_per_call": round(cold_ms, 5),
+        "cold_cache_ms_per_call": None if cold_ms is None else round(cold_ms, 5),
         "roofline": {
             "bound": "hbm",
             "achieved": round(achieved, 1),
