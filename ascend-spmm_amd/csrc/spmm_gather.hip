@@ -50,6 +50,9 @@ constexpr int kBatch = SPMM_GATHER_BATCH;  // dense rows per batch (two batches 
 constexpr int kStageUnroll = 8;             // staging loads issued per thread before storing
 // A row is "short" (summed by one lane group, never split) when it holds at
 // most R / SPMM_GATHER_SHORT_DIV nonzeros.
+#ifndef SPMM_GATHER_SPLIT_BYTES
+#define SPMM_GATHER_SPLIT_BYTES 512
+#endif
 #ifndef SPMM_GATHER_SHORT_DIV
 #define SPMM_GATHER_SHORT_DIV 2
 #endif
@@ -205,7 +208,7 @@ template <typename T, typename I>
 __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM_GATHER_WAVES))) void gather_tiles(
     Geometry<I> g, const I* __restrict__ col, const T* __restrict__ value,
     const T* __restrict__ dense, int64_t K, int64_t N, T* __restrict__ out, float* __restrict__ ws,
-    int log2L, int64_t chunks, int64_t ranges_per_tile, int64_t slot) {
+    int log2L, int64_t chunks, int64_t ranges_per_tile, int64_t slot, int wg_split) {
   constexpr int V = LaneVec<T>::V;
   extern __shared__ __align__(16) unsigned char smem[];
   // The tile's positions plus a halo of one range: a short row that starts
@@ -218,7 +221,12 @@ __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM
   // range boundary P0 + k*R, or -1.
   __shared__ int32_t s_cut[kTileRanges + 1];
 
-  const int64_t j0 = static_cast<int64_t>(blockIdx.x) * ranges_per_tile;
+  // wg_split > 1: the tile's column chunks go to wg_split work-groups (chunk
+  // = blockIdx % wg_split); consecutive blockIdx land on different XCDs, so
+  // each XCD's L2 serves one chunk of the dense rows.
+  const int64_t tile = static_cast<int64_t>(blockIdx.x) / wg_split;
+  const int64_t part = static_cast<int64_t>(blockIdx.x) % wg_split;
+  const int64_t j0 = tile * ranges_per_tile;
   const int64_t j1 = (j0 + ranges_per_tile < g.nranges) ? j0 + ranges_per_tile : g.nranges;
   const int64_t P0 = g.lo(j0), P1 = g.hi(j1 - 1);
   const int64_t base = g.rp(g.row_lo), end = g.rp(g.row_hi);
@@ -228,8 +236,8 @@ __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM
   // from the tile-row table of gather_tile_rows; tiles starting outside our
   // positions [base, end) clamp to the row range.  Runs of empty rows before
   // the tile are skipped.
-  const int64_t rS = P0 < base ? g.row_lo : (P0 < end ? g.tile_row[blockIdx.x] : g.row_hi);
-  const int64_t rE = P1 < base ? g.row_lo : (P1 < end ? g.tile_row[blockIdx.x + 1] + 1 : g.row_hi);
+  const int64_t rS = P0 < base ? g.row_lo : (P0 < end ? g.tile_row[tile] : g.row_hi);
+  const int64_t rE = P1 < base ? g.row_lo : (P1 < end ? g.tile_row[tile + 1] + 1 : g.row_hi);
 
   // Stage the tile's column ids and values (positions clamped to [0, nnz);
   // those outside our rows are never read) and clear the marks.  The loads
@@ -287,8 +295,9 @@ __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM
   const int L = 1 << log2L;
   const int group = threadIdx.x >> log2L;
   const int lane = threadIdx.x & (L - 1);
-  const int64_t j = j0 + group / chunks;
-  const int64_t cc = group % chunks;
+  const int64_t wg_chunks = chunks / wg_split;
+  const int64_t j = j0 + group / wg_chunks;
+  const int64_t cc = part * wg_chunks + group % wg_chunks;
   if (j >= j1) return;
   const bool reporter = lane == 0 && cc == 0;  // writes tail[j]
   const int64_t c0 = (cc * L + lane) * V;
@@ -479,12 +488,25 @@ spmm_status gather_typed(const void* rowptr, const void* col, const void* value,
   const int64_t lanes_needed = N / V;
   int log2L = 0;
   while ((1 << log2L) < lanes_needed && log2L < 6) ++log2L;
-  const int L = 1 << log2L;
-  const int64_t chunks = ceil_div(lanes_needed, L);
-  int64_t ranges_per_tile = (kWgThreads / L) / chunks;
+  int L = 1 << log2L;
+  int64_t chunks = ceil_div(lanes_needed, L);
+  // Dense rows of at least SPMM_GATHER_SPLIT_BYTES: one work-group per
+  // column chunk of a tile (rows of one chunk are halved first), so
+  // neighbouring work-groups, which run on different XCDs, gather different
+  // column pieces and each XCD's L2 holds a fraction of the dense operand.
+  int wg_split = 1;
+  if (SPMM_GATHER_SPLIT_BYTES > 0 && N * static_cast<int64_t>(sizeof(T)) >= SPMM_GATHER_SPLIT_BYTES) {
+    if (chunks == 1 && L >= 16 && lanes_needed == L) {
+      --log2L;
+      L >>= 1;
+      chunks = 2;
+    }
+    wg_split = static_cast<int>(chunks);
+  }
+  int64_t ranges_per_tile = (kWgThreads / L) / (chunks / wg_split);
   if (ranges_per_tile > kTileRanges) ranges_per_tile = kTileRanges;
   if (ranges_per_tile < 1) ranges_per_tile = 1;
-  const int64_t groups_per_wg = ranges_per_tile * chunks;
+  const int64_t groups_per_wg = ranges_per_tile * (chunks / wg_split);
   const int64_t wg_threads = groups_per_wg * L;
   const int64_t slot = gather_slot_floats(N);
 
@@ -506,11 +528,11 @@ spmm_status gather_typed(const void* rowptr, const void* col, const void* value,
     if (spmm_status st = check_launch("gather_tile_rows")) return st;
     const size_t lds = static_cast<size_t>((ranges_per_tile + 1) * g.range) *
                        (sizeof(I) + sizeof(T) + sizeof(int32_t));
-    hipLaunchKernelGGL((gather_tiles<T, I>), dim3(static_cast<unsigned>(tiles)),
+    hipLaunchKernelGGL((gather_tiles<T, I>), dim3(static_cast<unsigned>(tiles * wg_split)),
                        dim3(static_cast<unsigned>(wg_threads)), lds, stream, g,
                        static_cast<const I*>(col), static_cast<const T*>(value),
                        static_cast<const T*>(dense), K, N, static_cast<T*>(out), partial, log2L,
-                       chunks, ranges_per_tile, slot);
+                       chunks, ranges_per_tile, slot, wg_split);
     if (spmm_status st = check_launch("gather_tiles")) return st;
   }
   const int64_t fix_items = g.nnz > 0 ? (g.nranges - 1) * chunks * L : 0;
