@@ -21,11 +21,13 @@
 //    its row span from that table while it stages the tile's column ids and
 //    values in LDS (one round trip), then marks, per position, the row that
 //    starts there.  Each lane group then
-//    streams its range flat: the dense rows of 8 consecutive nonzeros are
+//    streams its range flat: the dense rows of 4 consecutive nonzeros are
 //    loaded together, two batches in flight (16 bytes per lane; the L lanes
 //    of a group read L*16 contiguous bytes of one dense row), accumulated in
-//    order, and flushed wherever the next position starts a new row.  Empty
-//    rows are written as zeros.
+//    order, and flushed wherever the next position starts a new row.  Each
+//    staged nonzero is one 16-byte LDS entry (column checked against K once,
+//    value bits, row mark), so a position costs one LDS read and 32-bit
+//    address arithmetic.  Empty rows are written as zeros.
 //  * A short row (at most R/2 nonzeros) is summed entirely by the lane group
 //    of the range where it starts (running on into the next range, staged as
 //    a halo); the next range skips it.  So every such row is one
@@ -44,7 +46,7 @@ using lanes::clampi;
 
 constexpr int kWgThreads = 256;
 #ifndef SPMM_GATHER_BATCH
-#define SPMM_GATHER_BATCH 8
+#define SPMM_GATHER_BATCH 4
 #endif
 constexpr int kBatch = SPMM_GATHER_BATCH;  // dense rows per batch (two batches in flight)
 constexpr int kStageUnroll = 8;             // staging loads issued per thread before storing
@@ -98,113 +100,134 @@ struct Geometry {
   }
 };
 
-// One batch of kBatch consecutive nonzeros: raw 16-byte dense pieces, values,
-// row marks (0 past the range end) and column validity.
+// LDS entry of one staged nonzero (16 bytes, read with one ds_read_b128):
+//   x: column id, or kBadCol when it is outside [0, K)
+//   y: value bits (fp16 zero-extended, or fp32)
+//   z: row mark, (row + 1 - rS) << 2 | to_vpart << 1 | ends_here, where the
+//      row part is set only at the position a row starts
+constexpr uint32_t kBadCol = 0xFFFFFFFFu;
+
+template <typename T>
+__device__ inline uint32_t value_bits(T v) {
+  if constexpr (sizeof(T) == 2)
+    return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, v));
+  else
+    return __builtin_bit_cast(uint32_t, v);
+}
+template <typename T>
+__device__ inline float bits_value(uint32_t b) {
+  if constexpr (sizeof(T) == 2)
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(b)));
+  else
+    return __builtin_bit_cast(float, b);
+}
+
+// One batch of kBatch consecutive nonzeros: raw 16-byte dense pieces, values
+// and row marks.  Positions past the range end or with an invalid column
+// carry value -0 and a zero dense piece, so their FMA adds exactly -0 (the
+// identity of fp32 addition); positions past the range end carry mark 0.
 template <typename T>
 struct Batch {
   lanes::raw16_t x[kBatch];
   float v[kBatch];
   int32_t m[kBatch];
-  bool ok[kBatch];
+  uint32_t ok;  // bit u: position u has a dense piece to use
 };
 
-// Issues the dense loads of a batch from the LDS-staged column ids; the row
-// marks are read from LDS here too, so accumulation never waits on LDS.
-template <typename T, typename I>
+// Issues the dense loads of a batch from the LDS entries.  Positions are
+// relative to the tile start.  Branch-free so the loads of a batch stay in
+// flight together: skipped positions load dense row 0 (K >= 1 here).
+template <typename T>
 struct Stream {
-  const I* s_col;
-  const T* s_val;
-  const int32_t* s_mark;
-  const T* dense;
-  int64_t K, N, c0, P0, pe;
+  const lanes::raw16_t* s_ent;
+  const T* dense_c0;  // dense + c0
+  uint32_t N;
+  int32_t pe;
 
-  // Branch-free so the loads of a batch stay in flight together: positions
-  // past the range end and invalid columns load dense row 0 (K >= 1 here)
-  // and are masked out by `ok`; positions past the range end get mark 0.
-  __device__ inline void issue(Batch<T>& b, int64_t p0) const {
+  __device__ inline void issue(Batch<T>& b, int32_t p0) const {
+    b.ok = 0;
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
-      const int64_t p = p0 + u;
+      const int32_t p = p0 + u;
       const bool in = p < pe;
-      const int64_t q = (in ? p : pe - 1) - P0;
-      const int64_t c = static_cast<int64_t>(s_col[q]);
-      const int32_t m = s_mark[q];
-      b.v[u] = static_cast<float>(s_val[q]);
-      b.m[u] = in ? m : 0;
-      b.ok[u] = in && static_cast<uint64_t>(c) < static_cast<uint64_t>(K);
-      b.x[u] = lanes::load_raw16(dense + (b.ok[u] ? c : 0) * N + c0);
+      const lanes::raw16_t e = s_ent[in ? p : pe - 1];
+      const bool ok = in && e.x != kBadCol;
+      b.ok |= ok ? 1u << u : 0u;
+      b.v[u] = ok ? bits_value<T>(e.y) : -0.0f;
+      b.m[u] = in ? static_cast<int32_t>(e.z) : 0;
+      const uint64_t off = static_cast<uint64_t>(ok ? e.x : 0u) * N;
+      b.x[u] = lanes::load_raw16(dense_c0 + off);
     }
   }
 };
 
-// Accumulates batches in position order.  Per tile position the LDS mark is
-// (row + 1 - rS) << 2 | to_vpart << 1 | ends_here, where the row part is set
-// only at the position a row starts: it tracks the current row, routes rows
-// of block windows to vpart, and flushes at row ends.
+// Accumulates batches in position order: tracks the current row from the
+// marks, routes rows of block windows to vpart, and flushes at row ends.
 template <typename T>
 struct Sink {
-  const int32_t* s_mark;
-  int64_t P0, pe, rS, row_hi;
+  const lanes::raw16_t* s_ent;
+  int64_t rS, row_hi;
   T* out;
   int64_t N, c0;
   float* vpart;
   float* head_slot;
   float* tail_slot;
-  int64_t row;             // row in progress, -1 while it is one started before the range
+  int32_t rel;             // row in progress + 1 - rS; 0 while it is one started before the range
   bool to_vpart;           // the row in progress belongs to a block window
   float acc[lanes::LaneVec<T>::V];
 
-  // Positions past the range end carry mark 0 and ok = false: no-ops.
+  __device__ inline void flush() {
+    constexpr int V = lanes::LaneVec<T>::V;
+    const int64_t row = rS + rel - 1;
+    // fp32 destinations: the head slot (row begun before the range) and
+    // vpart (block-window rows); others are rounded into out.
+    if (row < row_hi) {
+      if (rel == 0 || to_vpart) {
+        float* dst = rel == 0 ? head_slot : vpart + row * N + c0;
+#pragma unroll
+        for (int i = 0; i < V; ++i) dst[i] = acc[i];
+      } else {
+        lanes::LaneVec<T>::store(out + row * N + c0, acc);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[i] = 0.f;
+  }
+
   __device__ inline void consume(const Batch<T>& b) {
     constexpr int V = lanes::LaneVec<T>::V;
+    const lanes::raw16_t zero = {0u, 0u, 0u, 0u};
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
       const int32_t m = b.m[u];
       const int32_t start = m >> 2;
-      row = start ? rS + start - 1 : row;
+      rel = start ? start : rel;
       to_vpart = start ? (m & 2) != 0 : to_vpart;
       float x[V];
-      lanes::LaneVec<T>::unpack(b.x[u], x);
+      lanes::LaneVec<T>::unpack((b.ok >> u & 1u) ? b.x[u] : zero, x);
 #pragma unroll
-      for (int i = 0; i < V; ++i) {
-        const float t = __builtin_fmaf(b.v[u], x[i], acc[i]);
-        acc[i] = b.ok[u] ? t : acc[i];
-      }
-      if (m & 1) {
-        // fp32 destinations: the head slot (row begun before the range) and
-        // vpart (block-window rows); others are rounded into out.
-        if (row < row_hi) {
-          if (row < 0 || to_vpart) {
-            float* dst = row < 0 ? head_slot : vpart + row * N + c0;
-#pragma unroll
-            for (int i = 0; i < V; ++i) dst[i] = acc[i];
-          } else {
-            lanes::LaneVec<T>::store(out + row * N + c0, acc);
-          }
-        }
-#pragma unroll
-        for (int i = 0; i < V; ++i) acc[i] = 0.f;
-      }
+      for (int i = 0; i < V; ++i) acc[i] = __builtin_fmaf(b.v[u], x[i], acc[i]);
+      if (m & 1) flush();
     }
   }
 
   // The row in progress at the range end continues into the next range:
   // returns that row if it started in this range (a tail), else -1.
-  __device__ inline int64_t finish() {
+  __device__ inline int64_t finish(int32_t pe) {
     constexpr int V = lanes::LaneVec<T>::V;
-    if (s_mark[pe - 1 - P0] & 1) return -1;
-    float* dst = row < 0 ? head_slot : tail_slot;
+    if (s_ent[pe - 1].z & 1u) return -1;
+    float* dst = rel == 0 ? head_slot : tail_slot;
 #pragma unroll
     for (int i = 0; i < V; ++i) dst[i] = acc[i];
-    return row;
+    return rel == 0 ? -1 : rS + rel - 1;
   }
 };
 
-template <typename T, typename I>
 #ifndef SPMM_GATHER_WAVES
-#define SPMM_GATHER_WAVES 4
+#define SPMM_GATHER_WAVES 5
 #endif
 // Waves per SIMD the register budget of gather_tiles is fitted to.
+template <typename T, typename I>
 __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM_GATHER_WAVES))) void gather_tiles(
     Geometry<I> g, const I* __restrict__ col, const T* __restrict__ value,
     const T* __restrict__ dense, int64_t K, int64_t N, T* __restrict__ out, float* __restrict__ ws,
@@ -214,9 +237,8 @@ __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM
   // The tile's positions plus a halo of one range: a short row that starts
   // in the tile's last range is finished from the halo.
   const int64_t tile_positions = (ranges_per_tile + 1) * g.range;
-  I* s_col = reinterpret_cast<I*>(smem);
-  T* s_val = reinterpret_cast<T*>(smem + tile_positions * sizeof(I));
-  int32_t* s_mark = reinterpret_cast<int32_t*>(smem + tile_positions * (sizeof(I) + sizeof(T)));
+  lanes::raw16_t* s_ent = reinterpret_cast<lanes::raw16_t*>(smem);
+  uint32_t* s_word = reinterpret_cast<uint32_t*>(smem);  // s_word[4*i + 2] = mark of entry i
   // s_cut[k]: end (relative to P0) of the short row crossing the tile's k-th
   // range boundary P0 + k*R, or -1.
   __shared__ int32_t s_cut[kTileRanges + 1];
@@ -239,10 +261,10 @@ __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM
   const int64_t rS = P0 < base ? g.row_lo : (P0 < end ? g.tile_row[tile] : g.row_hi);
   const int64_t rE = P1 < base ? g.row_lo : (P1 < end ? g.tile_row[tile + 1] + 1 : g.row_hi);
 
-  // Stage the tile's column ids and values (positions clamped to [0, nnz);
-  // those outside our rows are never read) and clear the marks.  The loads
-  // do not wait for the row lookups above; each thread issues its loads
-  // before the first LDS store.
+  // Stage the tile's nonzeros as LDS entries (positions clamped to [0, nnz);
+  // those outside our rows are never read), column ids checked against K
+  // once here, marks cleared.  The loads do not wait for the row lookups
+  // above; each thread issues its loads before the first LDS store.
   const int64_t nr = j1 - j0;
   if (threadIdx.x <= nr) s_cut[threadIdx.x] = -1;
   for (int64_t i0 = 0; i0 < tile_positions; i0 += kStageUnroll * blockDim.x) {
@@ -259,9 +281,9 @@ __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM
     for (int k = 0; k < kStageUnroll; ++k) {
       const int64_t i = i0 + k * blockDim.x + threadIdx.x;
       if (i < tile_positions) {
-        s_mark[i] = 0;
-        s_col[i] = cs[k];
-        s_val[i] = vs[k];
+        const int64_t c = static_cast<int64_t>(cs[k]);
+        const uint32_t c32 = static_cast<uint64_t>(c) < static_cast<uint64_t>(K) ? static_cast<uint32_t>(c) : kBadCol;
+        s_ent[i] = lanes::raw16_t{c32, value_bits<T>(vs[k]), 0u, 0u};
       }
     }
   }
@@ -269,20 +291,19 @@ __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM
   // Mark the starts and ends of the tile's non-empty rows (ends also in the
   // halo); each position is marked only by the row that holds it.  A short
   // row (at most R / SPMM_GATHER_SHORT_DIV nonzeros) that crosses a range
-  // boundary is owned by the
-  // range where it starts: s_cut tells that range how far to run on and the
-  // next range where to begin.  Longer rows leave one fp32 partial per range
-  // instead.  Empty rows are left to the post pass.
+  // boundary is owned by the range where it starts: s_cut tells that range
+  // how far to run on and the next range where to begin.  Longer rows leave
+  // one fp32 partial per range instead.  Empty rows are left to the post pass.
   for (int64_t r = rS + threadIdx.x; r < rE; r += blockDim.x) {
     const int64_t a = g.rp(r), b = g.rp(r + 1);
     if (a < b) {
       const bool start_in = a >= P0 && a < P1 && r - rS < (INT32_MAX >> 2) - 1;
       const bool end_in = b - 1 >= P0 && b - 1 < P0 + tile_positions;
       if (start_in) {
-        const int32_t vp = g.in_block_window(r) ? 2 : 0;
-        s_mark[a - P0] = static_cast<int32_t>((r - rS + 1) << 2) | vp | (end_in && b - 1 == a ? 1 : 0);
+        const uint32_t vp = g.in_block_window(r) ? 2u : 0u;
+        s_word[4 * (a - P0) + 2] = static_cast<uint32_t>((r - rS + 1) << 2) | vp | (end_in && b - 1 == a ? 1u : 0u);
       }
-      if (end_in && !(start_in && b - 1 == a)) s_mark[b - 1 - P0] = 1;
+      if (end_in && !(start_in && b - 1 == a)) s_word[4 * (b - 1 - P0) + 2] = 1u;
       if (b - a <= g.range / SPMM_GATHER_SHORT_DIV) {
         const int64_t k = a < P0 ? 0 : (a - P0) / g.range + 1;  // first boundary after a
         if (k <= nr && P0 + k * g.range < b) s_cut[k] = static_cast<int32_t>(b - P0);
@@ -303,19 +324,18 @@ __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM
   const int64_t c0 = (cc * L + lane) * V;
   const int64_t lo = g.lo(j), hi = g.hi(j);
   // Skip the short row owned by the previous range; run on to the end of the
-  // short row this range owns past its end.
+  // short row this range owns past its end.  Positions from here on are
+  // relative to P0.
   const int32_t cut_in = s_cut[j - j0], cut_out = s_cut[j - j0 + 1];
-  const int64_t ps = cut_in >= 0 ? P0 + cut_in : (lo > base ? lo : base);
-  const int64_t pe = cut_out >= 0 ? P0 + cut_out : (hi < end ? hi : end);
+  const int32_t ps = cut_in >= 0 ? cut_in : static_cast<int32_t>((lo > base ? lo : base) - P0);
+  const int32_t pe = cut_out >= 0 ? cut_out : static_cast<int32_t>((hi < end ? hi : end) - P0);
   if (ps >= pe || c0 >= N) {
     if (reporter) g.tail[j] = -1;
     return;
   }
 
   Sink<T> sk;
-  sk.s_mark = s_mark;
-  sk.P0 = P0;
-  sk.pe = pe;
+  sk.s_ent = s_ent;
   sk.rS = rS;
   sk.row_hi = g.row_hi;
   sk.out = out;
@@ -325,49 +345,41 @@ __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM
   sk.to_vpart = false;
   sk.head_slot = ws + (2 * j) * slot + c0;
   sk.tail_slot = ws + (2 * j + 1) * slot + c0;
-  sk.row = -1;  // set by the first row-start mark; stays -1 for a row begun earlier
+  sk.rel = 0;  // set by the first row-start mark; stays 0 for a row begun earlier
 #pragma unroll
   for (int i = 0; i < V; ++i) sk.acc[i] = 0.f;
 
-  int64_t tail_row;
   if (K <= 0) {  // no valid column: rows still flush (as zeros)
     Batch<T> z;
+    z.ok = 0;
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
-      z.ok[u] = false;
-      z.v[u] = 0.f;
+      z.v[u] = -0.0f;
       z.x[u] = lanes::raw16_t{0, 0, 0, 0};
     }
-    for (int u = 0; u < kBatch; ++u) z.m[u] = 0;
-    for (int64_t p0 = ps; p0 < pe; p0 += kBatch) {
+    for (int32_t p0 = ps; p0 < pe; p0 += kBatch) {
 #pragma unroll
-      for (int u = 0; u < kBatch; ++u) z.m[u] = p0 + u < pe ? s_mark[p0 + u - P0] : 0;
+      for (int u = 0; u < kBatch; ++u) z.m[u] = p0 + u < pe ? static_cast<int32_t>(s_ent[p0 + u].z) : 0;
       sk.consume(z);
     }
-    tail_row = sk.finish();
   } else {
     // Two batches of kBatch dense rows in flight: the loads of batch k+1 are
     // issued before batch k is accumulated.
-    Stream<T, I> st;
-    st.s_col = s_col;
-    st.s_val = s_val;
-    st.s_mark = s_mark;
-    st.dense = dense;
-    st.K = K;
-    st.N = N;
-    st.c0 = c0;
-    st.P0 = P0;
+    Stream<T> st;
+    st.s_ent = s_ent;
+    st.dense_c0 = dense + c0;
+    st.N = static_cast<uint32_t>(N);
     st.pe = pe;
     Batch<T> ba, bb;
     st.issue(ba, ps);
-    for (int64_t p0 = ps; p0 < pe; p0 += 2 * kBatch) {
+    for (int32_t p0 = ps; p0 < pe; p0 += 2 * kBatch) {
       st.issue(bb, p0 + kBatch);
       sk.consume(ba);
       st.issue(ba, p0 + 2 * kBatch);
       sk.consume(bb);
     }
-    tail_row = sk.finish();
   }
+  const int64_t tail_row = sk.finish(pe);
   if (reporter) g.tail[j] = tail_row;
 }
 
@@ -485,6 +497,8 @@ spmm_status gather_typed(const void* rowptr, const void* col, const void* value,
   g.climit = climit;
   g.vpart = vpart;
 
+  if (K > static_cast<int64_t>(kBadCol) - 1)
+    return fail(SPMM_ERR_CONTRACT, "dense has too many rows for 32-bit column ids");
   const int64_t lanes_needed = N / V;
   int log2L = 0;
   while ((1 << log2L) < lanes_needed && log2L < 6) ++log2L;
@@ -526,8 +540,7 @@ spmm_status gather_typed(const void* rowptr, const void* col, const void* value,
     hipLaunchKernelGGL((gather_tile_rows<I>), dim3(static_cast<unsigned>(ceil_div(row_hi - row_lo, kWgThreads))),
                        dim3(kWgThreads), 0, stream, g, ranges_per_tile * g.range, tiles);
     if (spmm_status st = check_launch("gather_tile_rows")) return st;
-    const size_t lds = static_cast<size_t>((ranges_per_tile + 1) * g.range) *
-                       (sizeof(I) + sizeof(T) + sizeof(int32_t));
+    const size_t lds = static_cast<size_t>((ranges_per_tile + 1) * g.range) * sizeof(lanes::raw16_t);
     hipLaunchKernelGGL((gather_tiles<T, I>), dim3(static_cast<unsigned>(tiles * wg_split)),
                        dim3(static_cast<unsigned>(wg_threads)), lds, stream, g,
                        static_cast<const I*>(col), static_cast<const T*>(value),
