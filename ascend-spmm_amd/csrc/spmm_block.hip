@@ -53,9 +53,6 @@ typedef float float4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kXcds = 8;
 
-#ifndef SPMM_BLOCK_PIPELINE
-#define SPMM_BLOCK_PIPELINE 0
-#endif
 
 // Arguments shared by the block kernels.
 template <typename T, typename I>
@@ -82,23 +79,42 @@ struct BlockArgs {
   __device__ inline bool row_has_vector(int64_t r) const { return r < vrows && vrp(r) != vrp(r + 1); }
 };
 
-// LDS staging of one chunk of blocks [b0, b1) (b1 - b0 <= kbig): the block
-// columns and the 16 values of every block, loaded with coalesced 16-byte
-// pieces (Cvalue is 16-byte aligned by contract).  With `finish` set it also
-// returns the window's vector-row bits (bit r: row 16*s + r has vector-part
-// nonzeros, whose fp32 sum is in vpart), read in the same round trip.
+constexpr uint32_t kBadCol = 0xFFFFFFFFu;  // staged column id of an invalid block
+
+// K-step of the MFMA loop: blocks per step (fp16 16x16x32 takes 8 blocks per
+// lane group of 16 lanes, fp32 16x16x4 takes 4).
+template <typename T>
+constexpr int64_t k_step() { return sizeof(T) == 2 ? 32 : 16; }
+
+// LDS staging of one chunk of blocks [b0, b1) (b1 - b0 <= stage): the block
+// columns, checked against K here once (kBadCol when out of range), and the
+// 16 values of every block, loaded with coalesced 16-byte pieces (Cvalue is
+// 16-byte aligned by contract).  The chunk is padded to a whole K-step with
+// kBadCol columns and zero values, so the MFMA loop reads LDS without bounds
+// checks.  With `finish` set it also returns the window's vector-row bits
+// (bit r: row 16*s + r has vector-part nonzeros, whose fp32 sum is in vpart),
+// read in the same round trip.
 template <typename T, typename I>
 __device__ inline unsigned stage_chunk(const BlockArgs<T, I>& a, int64_t s, bool finish, int64_t b0,
-                                       int64_t b1, I* s_col, T* s_val) {
+                                       int64_t b1, uint32_t* s_col, T* s_val) {
   __shared__ unsigned s_vec;
   const int64_t n = b1 - b0;
+  const int64_t n_pad = (n + k_step<T>() - 1) / k_step<T>() * k_step<T>();
   if (threadIdx.x == 0) s_vec = 0;
   const bool vec = finish && threadIdx.x < 16 && a.row_has_vector(16 * s + threadIdx.x);
-  for (int64_t i = threadIdx.x; i < n; i += blockDim.x) s_col[i] = a.Ccol[b0 + i];
+  for (int64_t i = threadIdx.x; i < n_pad; i += blockDim.x) {
+    uint32_t c = kBadCol;
+    if (i < n) {
+      const int64_t cv = static_cast<int64_t>(a.Ccol[b0 + i]);
+      c = static_cast<uint64_t>(cv) < static_cast<uint64_t>(a.K) ? static_cast<uint32_t>(cv) : kBadCol;
+    }
+    s_col[i] = c;
+  }
   constexpr int64_t kPer = 16 * sizeof(T) / 16;  // 16-byte pieces per block
   const lanes::raw16_t* src = reinterpret_cast<const lanes::raw16_t*>(a.Cvalue + 16 * b0);
   lanes::raw16_t* dst = reinterpret_cast<lanes::raw16_t*>(s_val);
-  for (int64_t i = threadIdx.x; i < n * kPer; i += blockDim.x) dst[i] = src[i];
+  for (int64_t i = threadIdx.x; i < n_pad * kPer; i += blockDim.x)
+    dst[i] = i < n * kPer ? src[i] : lanes::raw16_t{0u, 0u, 0u, 0u};
   __syncthreads();
   if (vec) atomicOr(&s_vec, 1u << threadIdx.x);
   __syncthreads();
@@ -106,8 +122,8 @@ __device__ inline unsigned stage_chunk(const BlockArgs<T, I>& a, int64_t s, bool
 }
 
 // One K-step of dense rows per lane, loaded before the step is multiplied.
-// Lanes of blocks past the chunk end or with an invalid column get zeros
-// (never a load), so padding contributes exactly nothing.
+// Lanes of padding blocks or blocks with an invalid column get zeros (never a
+// load), so they contribute exactly nothing.
 template <typename T> struct StepRows;
 template <> struct StepRows<_Float16> {  // 8 blocks x 4 columns per lane (K-step 32)
   half4_t r[8];
@@ -119,102 +135,59 @@ template <> struct StepRows<float> {  // 4 blocks x 4 columns per lane (K-step 1
 // MFMA sum of staged blocks [0, n) for the 64-column group at n0.  Lane
 // (q = lane % 16, kg = lane / 16) loads columns n0+4q .. n0+4q+3 of its
 // blocks' dense rows; MFMA j uses element j, so the accumulator lane holds 4
-// consecutive output columns (rows 4kg .. 4kg+3).  Dense loads run one K-step
-// ahead of the MFMAs.  Adds to `acc`.
+// consecutive output columns (rows 4kg .. 4kg+3).  Adds to `acc`.
 template <typename T, typename I>
-__device__ inline void group_sum(const BlockArgs<T, I>& a, const I* s_col, const T* s_val, int64_t n,
-                                 int64_t n0, int lane, float4_t (&acc)[4]) {
+__device__ inline void group_sum(const BlockArgs<T, I>& a, const uint32_t* s_col, const T* s_val,
+                                 int64_t n, int64_t n0, int lane, float4_t (&acc)[4]) {
   const int q = lane & 15, kg = lane >> 4;
   const bool col_ok = (n0 + 4 * q) < a.N;
-  const int64_t coff = n0 + 4 * q;
+  const T* dense_q = a.dense + n0 + 4 * q;
+  const uint32_t Nu = static_cast<uint32_t>(a.N);
   if (a.K <= 0 || n <= 0) return;  // uniform: no valid dense row
+  const int32_t steps = static_cast<int32_t>((n + k_step<T>() - 1) / k_step<T>());
   if constexpr (sizeof(T) == 2) {
-    constexpr int64_t kStep = 32;
-    auto issue = [&](StepRows<_Float16>& st, int64_t k0) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int64_t blk = k0 + 8 * kg + e;
-        const int64_t c = blk < n ? static_cast<int64_t>(s_col[blk]) : -1;
-        if (col_ok && static_cast<uint64_t>(c) < static_cast<uint64_t>(a.K))
-          st.r[e] = *reinterpret_cast<const half4_t*>(a.dense + c * a.N + coff);
-        else
-          st.r[e] = half4_t{0, 0, 0, 0};
-      }
-    };
-    auto multiply = [&](const StepRows<_Float16>& st, int64_t k0) {
+    for (int32_t st = 0; st < steps; ++st) {
+      const int32_t k0 = st * 32 + 8 * kg;
+      StepRows<_Float16> rows;
       half8_t av;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const int64_t blk = k0 + 8 * kg + e;
-        av[e] = blk < n ? s_val[blk * 16 + q] : static_cast<_Float16>(0.f);
+        const uint32_t c = s_col[k0 + e];
+        av[e] = s_val[(k0 + e) * 16 + q];
+        if (col_ok && c != kBadCol)
+          rows.r[e] = *reinterpret_cast<const half4_t*>(dense_q + static_cast<uint64_t>(c) * Nu);
+        else
+          rows.r[e] = half4_t{0, 0, 0, 0};
       }
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         half8_t b;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) b[e] = st.r[e][j];
+        for (int e = 0; e < 8; ++e) b[e] = rows.r[e][j];
         acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b, acc[j], 0, 0, 0);
       }
-    };
-#if SPMM_BLOCK_PIPELINE
-    StepRows<_Float16> sa, sb;
-    issue(sa, 0);
-    for (int64_t k0 = 0; k0 < n; k0 += 2 * kStep) {
-      const bool more = k0 + kStep < n;
-      if (more) issue(sb, k0 + kStep);
-      multiply(sa, k0);
-      if (!more) break;
-      if (k0 + 2 * kStep < n) issue(sa, k0 + 2 * kStep);
-      multiply(sb, k0 + kStep);
     }
-#else
-    for (int64_t k0 = 0; k0 < n; k0 += kStep) {
-      StepRows<_Float16> sa;
-      issue(sa, k0);
-      multiply(sa, k0);
-    }
-#endif
   } else {
-    constexpr int64_t kStep = 16;
-    auto issue = [&](StepRows<float>& st, int64_t k0) {
+    for (int32_t st = 0; st < steps; ++st) {
+      StepRows<float> rows;
+      float av[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const int64_t blk = k0 + 4 * u + kg;
-        const int64_t c = blk < n ? static_cast<int64_t>(s_col[blk]) : -1;
-        if (col_ok && static_cast<uint64_t>(c) < static_cast<uint64_t>(a.K))
-          st.r[u] = *reinterpret_cast<const float4_t*>(a.dense + c * a.N + coff);
+        const int32_t blk = st * 16 + 4 * u + kg;
+        const uint32_t c = s_col[blk];
+        av[u] = s_val[blk * 16 + q];
+        if (col_ok && c != kBadCol)
+          rows.r[u] = *reinterpret_cast<const float4_t*>(dense_q + static_cast<uint64_t>(c) * Nu);
         else
-          st.r[u] = float4_t{0.f, 0.f, 0.f, 0.f};
+          rows.r[u] = float4_t{0.f, 0.f, 0.f, 0.f};
       }
-    };
-    auto multiply = [&](const StepRows<float>& st, int64_t k0) {
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const int64_t blk = k0 + 4 * u + kg;
-        const float av = blk < n ? s_val[blk * 16 + q] : 0.f;
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, st.r[u][j], acc[j], 0, 0, 0);
+          acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[u], rows.r[u][j], acc[j], 0, 0, 0);
       }
-    };
-#if SPMM_BLOCK_PIPELINE
-    StepRows<float> sa, sb;
-    issue(sa, 0);
-    for (int64_t k0 = 0; k0 < n; k0 += 2 * kStep) {
-      const bool more = k0 + kStep < n;
-      if (more) issue(sb, k0 + kStep);
-      multiply(sa, k0);
-      if (!more) break;
-      if (k0 + 2 * kStep < n) issue(sa, k0 + 2 * kStep);
-      multiply(sb, k0 + kStep);
     }
-#else
-    for (int64_t k0 = 0; k0 < n; k0 += kStep) {
-      StepRows<float> sa;
-      issue(sa, k0);
-      multiply(sa, k0);
-    }
-#endif
   }
 }
 
@@ -238,7 +211,7 @@ __device__ inline unsigned window_vector_rows(const BlockArgs<T, I>& a, int64_t 
 // not depend on it); a window that fits is staged once for all column groups.
 template <typename T, typename I>
 __device__ inline void window_chunk(const BlockArgs<T, I>& a, int64_t s, int64_t b0, int64_t b1,
-                                    float* slot, I* s_col, T* s_val) {
+                                    float* slot, uint32_t* s_col, T* s_val) {
   const int64_t n = b1 - b0;
   const bool once = n <= a.stage;
   unsigned vec = 0;
@@ -332,7 +305,7 @@ template <typename T, typename I>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SPMM_BLOCK_WAVES))) void block_windows(BlockArgs<T, I> a) {
   extern __shared__ __align__(16) unsigned char smem[];
   T* s_val = reinterpret_cast<T*>(smem);                           // [stage][16]
-  I* s_col = reinterpret_cast<I*>(smem + a.stage * 16 * sizeof(T));  // [stage]
+  uint32_t* s_col = reinterpret_cast<uint32_t*>(smem + a.stage * 16 * sizeof(T));  // [stage]
   const int64_t lead = a.per_xcd * kXcds;
   const int64_t g = blockIdx.x;
   const int64_t n16 = 16 * a.N;
@@ -395,6 +368,8 @@ spmm_status block_typed(const void* Crowptr, const void* Ccol, const void* Cvalu
                         int64_t vector_rows, int64_t vector_nnz, const void* dense, int64_t K,
                         int64_t N, void* out, const float* vpart, float* slots, hipStream_t stream) {
   if (windows <= 0) return SPMM_OK;
+  if (K > static_cast<int64_t>(kBadCol) - 1)
+    return fail(SPMM_ERR_CONTRACT, "dense has too many rows for 32-bit column ids");
   BlockArgs<T, I> a;
   a.Crowptr = static_cast<const I*>(Crowptr);
   a.Ccol = static_cast<const I*>(Ccol);
@@ -421,7 +396,7 @@ spmm_status block_typed(const void* Crowptr, const void* Ccol, const void* Cvalu
   const int64_t mean = a.limit / windows;
   a.stage = 64;
   while (a.stage < 2 * mean && a.stage < a.kbig) a.stage *= 2;
-  const size_t stage_lds = static_cast<size_t>(a.stage) * (16 * sizeof(T) + sizeof(I));
+  const size_t stage_lds = static_cast<size_t>(a.stage) * (16 * sizeof(T) + sizeof(uint32_t));
   const int64_t grid = a.per_xcd * kXcds + a.noverflow;
   hipLaunchKernelGGL((block_windows<T, I>), dim3(static_cast<unsigned>(grid)), dim3(64 * waves),
                      stage_lds, stream, a);

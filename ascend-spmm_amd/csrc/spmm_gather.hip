@@ -48,7 +48,11 @@ constexpr int kWgThreads = 256;
 #ifndef SPMM_GATHER_BATCH
 #define SPMM_GATHER_BATCH 4
 #endif
-constexpr int kBatch = SPMM_GATHER_BATCH;  // dense rows per batch (two batches in flight)
+constexpr int kBatch = SPMM_GATHER_BATCH;  // dense rows per batch
+#ifndef SPMM_GATHER_INFLIGHT
+#define SPMM_GATHER_INFLIGHT 2
+#endif
+constexpr int kInFlight = SPMM_GATHER_INFLIGHT;  // batches in flight per lane group
 constexpr int kStageUnroll = 8;             // staging loads issued per thread before storing
 // A row is "short" (summed by one lane group, never split) when it holds at
 // most R / SPMM_GATHER_SHORT_DIV nonzeros.
@@ -363,20 +367,22 @@ __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM
       sk.consume(z);
     }
   } else {
-    // Two batches of kBatch dense rows in flight: the loads of batch k+1 are
-    // issued before batch k is accumulated.
+    // kInFlight batches of kBatch dense rows in flight: the loads of the
+    // next kInFlight-1 batches are issued before a batch is accumulated.
     Stream<T> st;
     st.s_ent = s_ent;
     st.dense_c0 = dense + c0;
     st.N = static_cast<uint32_t>(N);
     st.pe = pe;
-    Batch<T> ba, bb;
-    st.issue(ba, ps);
-    for (int32_t p0 = ps; p0 < pe; p0 += 2 * kBatch) {
-      st.issue(bb, p0 + kBatch);
-      sk.consume(ba);
-      st.issue(ba, p0 + 2 * kBatch);
-      sk.consume(bb);
+    Batch<T> bq[kInFlight];
+#pragma unroll
+    for (int k = 0; k + 1 < kInFlight; ++k) st.issue(bq[k], ps + k * kBatch);
+    for (int32_t p0 = ps; p0 < pe; p0 += kInFlight * kBatch) {
+#pragma unroll
+      for (int k = 0; k < kInFlight; ++k) {
+        st.issue(bq[(k + kInFlight - 1) % kInFlight], p0 + (k + kInFlight - 1) * kBatch);
+        sk.consume(bq[k]);
+      }
     }
   }
   const int64_t tail_row = sk.finish(pe);

@@ -6,11 +6,12 @@ N=128 fp16, fp32 accumulate) — the configuration the headline metric
 A step is one SpMM call over resident device inputs.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 2] [--width N]
-                       [--op csr|mixed|mixed-empty|graph] [--no-cpu] [--no-block-path] [--no-cold]
+                       [--op csr|mixed|mixed-empty|bcsr|graph] [--no-cpu] [--no-block-path] [--no-cold]
        python bench.py --copy-calibration
 
 ``--op mixed`` times ``spmm_ascend_cube`` on the output of the GPU
 ``preprocess`` (block windows on MFMA, the rest on the gather path); ``--op
+bcsr`` on the output of ``csr_to_bcsr`` (every window on MFMA); ``--op
 graph`` times pack_node_tensor -> spmm_ascend_cube on P A P^T ->
 restore_node_tensor (``preprocess(graph_layout=True)``).  Unless
 ``--no-block-path`` is given, the line also carries ``block_path``: config 3
@@ -107,29 +108,39 @@ def cpu_baseline(w, B: np.ndarray, budget_s: float) -> dict:
 
 def time_calls(step, steps: int, warmup: int, cold: bool = False):
     """Wall ms per step over `steps` back-to-back calls (synchronised on both
-    sides) and the mean HIP-event ms per call, events recorded on the stream
-    the ops launch on (torch's current stream).  With cold=True, a 512 MiB
-    scratch write runs between calls to evict L2 and the Infinity Cache, and
-    only the events count."""
+    sides) and the HIP-event ms per call, events recorded on the stream the
+    ops launch on (torch's current stream).  Warm: one event pair brackets
+    the whole loop, so no timing marker sits between calls.  With cold=True,
+    a 512 MiB scratch write runs before every call to evict L2 and the
+    Infinity Cache, and each call is bracketed by its own event pair."""
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
+    if not cold:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        e0.record(stream)
+        for _ in range(steps):
+            step()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+        return wall_ms, e0.elapsed_time(e1) / steps
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
           for _ in range(steps)]
-    scratch = torch.empty(512 * 1024 * 1024, dtype=torch.uint8, device="cuda") if cold else None
+    scratch = torch.empty(512 * 1024 * 1024, dtype=torch.uint8, device="cuda")
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(steps):
-        if scratch is not None:
-            scratch.fill_(i & 0xFF)
+        scratch.fill_(i & 0xFF)
         ev[i][0].record(stream)
         step()
         ev[i][1].record(stream)
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / steps
-    event_ms = float(np.mean([a.elapsed_time(b) for a, b in ev]))
-    return wall_ms, event_ms
+    return wall_ms, float(np.mean([a.elapsed_time(b) for a, b in ev]))
 
 
 def device_csr(w, dev):
@@ -154,29 +165,42 @@ def mixed_operands(spmm_npu, w, dev, graph_layout: bool):
 
 
 def block_path(spmm_npu, dev, steps: int, warmup: int) -> dict:
-    """Config 3 (block-banded) at N=128 fp16: spmm_ascend_cube after the GPU
-    preprocess against spmm_csr on the same matrix."""
+    """Config 3 (block-banded) at N=128 fp16: spmm_ascend_cube on the output
+    of the GPU preprocess (the reference's headline pipeline) and on the
+    output of csr_to_bcsr (every window on MFMA, the reference's AIC-only
+    configuration), each against spmm_csr on the same matrix."""
     w = workloads.make(3)
     width = 128
     dense = torch.from_numpy(w.dense(width)).to(dev)
     crow, col, val = device_csr(w, dev)
     start = spmm_npu.make_start(crow, 40).to(dev)
     ops, cstart, vstart, p = mixed_operands(spmm_npu, w, dev, False)
+    i32 = torch.int32
+    b = spmm_npu.csr_to_bcsr(crow, col, val, w.rows, w.cols, 16)
+    bops = (b["crow_window_ptr"].to(i32), b["unique_col_ids"].to(i32), b["value"],
+            torch.zeros(1, dtype=i32, device=dev), torch.zeros(0, dtype=i32, device=dev),
+            torch.zeros(0, dtype=val.dtype, device=dev))
+    bstart = spmm_npu.make_start(b["crow_window_ptr"], 20).to(dev)
     _, csr_ms = time_calls(lambda: spmm_npu.spmm_csr(crow, col, val, dense, start), steps, warmup)
     _, mixed_ms = time_calls(lambda: spmm_npu.spmm_ascend_cube(*ops, dense, cstart, vstart), steps, warmup)
+    _, bcsr_ms = time_calls(lambda: spmm_npu.spmm_ascend_cube(*bops, dense, bstart, start), steps, warmup)
     nblk = int(p["crow_window_ptr"][-1].item())
-    mfma_tflops = 2.0 * 16 * nblk * width / (mixed_ms / 1e3) / 1e12
+    nblk_all = int(b["crow_window_ptr"][-1].item())
+    mfma_tflops = 2.0 * 16 * nblk_all * width / (bcsr_ms / 1e3) / 1e12
     return {
         "workload": f"{w.name} {w.rows}x{w.cols} nnz={w.nnz} N={width} fp16",
         "spmm_csr_ms": round(csr_ms, 5),
-        "spmm_ascend_cube_ms": round(mixed_ms, 5),
-        "speedup_vs_spmm_csr": round(csr_ms / mixed_ms, 3),
-        "gflops": round(2.0 * w.nnz * width / (mixed_ms / 1e3) / 1e9, 1),
-        "aic_windows": int(p["crow_window_ptr"].numel() - 1),
-        "aic_blocks_16x1": nblk,
-        "vector_nnz": int(p["vvalue"].numel()),
-        "mfma_executed_tflops": round(mfma_tflops, 2),
-        "mfma_utilisation": round(mfma_tflops / MFMA_PEAK_TFLOPS["fp16"], 4),
+        "preprocess_spmm_ascend_cube_ms": round(mixed_ms, 5),
+        "speedup_preprocess_vs_spmm_csr": round(csr_ms / mixed_ms, 3),
+        "bcsr_spmm_ascend_cube_ms": round(bcsr_ms, 5),
+        "speedup_bcsr_vs_spmm_csr": round(csr_ms / bcsr_ms, 3),
+        "gflops_bcsr": round(2.0 * w.nnz * width / (bcsr_ms / 1e3) / 1e9, 1),
+        "preprocess_aic_windows": int(p["crow_window_ptr"].numel() - 1),
+        "preprocess_aic_blocks_16x1": nblk,
+        "preprocess_vector_nnz": int(p["vvalue"].numel()),
+        "bcsr_blocks_16x1": nblk_all,
+        "bcsr_mfma_executed_tflops": round(mfma_tflops, 2),
+        "bcsr_mfma_utilisation": round(mfma_tflops / MFMA_PEAK_TFLOPS["fp16"], 4),
     }
 
 
@@ -197,7 +221,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", type=int, default=2)
     ap.add_argument("--width", type=int, default=None)
-    ap.add_argument("--op", choices=["csr", "mixed", "mixed-empty", "graph"], default="csr")
+    ap.add_argument("--op", choices=["csr", "mixed", "mixed-empty", "bcsr", "graph"], default="csr")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-block-path", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
@@ -242,6 +266,19 @@ def main() -> int:
         def step():
             return spmm_npu.spmm_ascend_cube(z1, e_i, e_v, crow, col, val, dense, z20, start)
         op_name = "spmm_ascend_cube(vector part only)"
+    elif args.op == "bcsr":
+        crow, col, val = device_csr(w, dev)
+        b = spmm_npu.csr_to_bcsr(crow, col, val, w.rows, w.cols, 16)
+        i32 = torch.int32
+        bops = (b["crow_window_ptr"].to(i32), b["unique_col_ids"].to(i32), b["value"],
+                torch.zeros(1, dtype=i32, device=dev), torch.zeros(0, dtype=i32, device=dev),
+                torch.zeros(0, dtype=val.dtype, device=dev))
+        cstart = spmm_npu.make_start(b["crow_window_ptr"], 20).to(dev)
+        vstart = torch.zeros(40, dtype=i32, device=dev)
+
+        def step():
+            return spmm_npu.spmm_ascend_cube(*bops, dense, cstart, vstart)
+        op_name = "csr_to_bcsr -> spmm_ascend_cube (block part only; conversion untimed)"
     elif args.op == "mixed":
         ops, cstart, vstart, _ = mixed_operands(spmm_npu, w, dev, False)
 
