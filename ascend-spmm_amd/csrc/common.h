@@ -73,10 +73,16 @@ spmm_status launch_gather(int32_t index_type, int32_t value_type,
 size_t gather_workspace_bytes(int64_t nnz, int64_t width);
 
 // Blocks of a window handled by one work-group before the window is split
-// (fixed per value type, so results do not depend on the width).
-template <typename T>
-constexpr int64_t block_chunk() { return sizeof(T) == 2 ? 512 : 256; }
-inline int64_t block_chunk_for(int32_t value_type) { return value_type == SPMM_VALUE_F16 ? 512 : 256; }
+// into chunks that separate work-groups sum and a combine pass adds in
+// order.  It grows with the total block count (at most about 16384 chunks,
+// 4096 blocks per chunk at most), so large inputs keep the partial sums (and
+// their workspace) small; it depends on the value type and the block count
+// only, never on the width, so results do not depend on the width.
+inline int64_t block_chunk_for(int32_t value_type, int64_t blocks) {
+  int64_t k = value_type == SPMM_VALUE_F16 ? 512 : 256;
+  while (k < 4096 && blocks / k > 16384) k *= 2;
+  return k;
+}
 
 // Number of fixed overflow ranges for `blocks` usable blocks.
 int64_t block_overflow_ranges(int64_t blocks, int64_t kbig);

@@ -25,8 +25,9 @@
 //  * Waves of the work-group take 64-column groups round-robin; each group
 //    runs the whole K loop, so every output element sees the same MFMA
 //    sequence for every width N.
-//  * Windows longer than a fixed chunk (block_chunk: 512 blocks fp16, 256
-//    fp32) are cut at fixed block positions: the window's own work-group
+//  * Windows longer than a chunk (block_chunk_for: 512 blocks fp16, 256
+//    fp32, growing with the total block count) are cut at fixed block
+//    positions: the window's own work-group
 //    takes its first chunk, and "overflow" work-groups take the rest in fixed
 //    global block ranges (only one window can overflow into a range).  A
 //    combine kernel adds the pieces in order, so the split is deterministic.
@@ -52,6 +53,12 @@ typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kXcds = 8;
+// Waves per window work-group: one per 64-column group, up to this many (the
+// rest loop), so wide outputs do not lengthen each wave's chain of K-steps.
+#ifndef SPMM_BLOCK_MAX_WAVES
+#define SPMM_BLOCK_MAX_WAVES 4
+#endif
+constexpr int kMaxWaves = SPMM_BLOCK_MAX_WAVES;
 
 
 // Arguments shared by the block kernels.
@@ -302,7 +309,7 @@ template <typename T, typename I>
 #define SPMM_BLOCK_WAVES 4
 #endif
 // Waves per SIMD the register budget of block_windows is fitted to.
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SPMM_BLOCK_WAVES))) void block_windows(BlockArgs<T, I> a) {
+__global__ __launch_bounds__(64 * kMaxWaves) __attribute__((amdgpu_waves_per_eu(SPMM_BLOCK_WAVES))) void block_windows(BlockArgs<T, I> a) {
   extern __shared__ __align__(16) unsigned char smem[];
   T* s_val = reinterpret_cast<T*>(smem);                           // [stage][16]
   uint32_t* s_col = reinterpret_cast<uint32_t*>(smem + a.stage * 16 * sizeof(T));  // [stage]
@@ -386,16 +393,18 @@ spmm_status block_typed(const void* Crowptr, const void* Ccol, const void* Cvalu
   a.out = static_cast<T*>(out);
   a.vpart = vpart;
   a.slots = slots;
-  a.kbig = block_chunk<T>();
+  a.kbig = block_chunk_for(sizeof(T) == 2 ? SPMM_VALUE_F16 : SPMM_VALUE_F32, a.limit);
   a.noverflow = block_overflow_ranges(a.limit, a.kbig);
   a.per_xcd = ceil_div(windows, kXcds);
   const int64_t groups = (N + 63) / 64;
-  const int waves = groups < 4 ? static_cast<int>(groups) : 4;
-  // Staging piece: about twice the mean window, 64 .. kbig blocks, so LDS per
-  // work-group stays small for small windows and most windows stage once.
+  const int waves = groups < kMaxWaves ? static_cast<int>(groups) : kMaxWaves;
+  // Staging piece: about twice the mean window, 64 blocks up to a 20 KB LDS
+  // budget (512 blocks fp16, 256 fp32), so LDS per work-group stays small for
+  // small windows and most windows stage once.
   const int64_t mean = a.limit / windows;
+  const int64_t stage_max = sizeof(T) == 2 ? 512 : 256;
   a.stage = 64;
-  while (a.stage < 2 * mean && a.stage < a.kbig) a.stage *= 2;
+  while (a.stage < 2 * mean && a.stage < a.kbig && a.stage < stage_max) a.stage *= 2;
   const size_t stage_lds = static_cast<size_t>(a.stage) * (16 * sizeof(T) + sizeof(uint32_t));
   const int64_t grid = a.per_xcd * kXcds + a.noverflow;
   hipLaunchKernelGGL((block_windows<T, I>), dim3(static_cast<unsigned>(grid)), dim3(64 * waves),

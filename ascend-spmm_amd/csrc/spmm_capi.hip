@@ -123,7 +123,7 @@ struct MixedLayout {
     vpart = align_up(static_cast<size_t>(16 * windows) * w * sizeof(float), 256);
     limit = d->block_count < d->block_values / 16 ? d->block_count : d->block_values / 16;
     if (limit < 0) limit = 0;
-    const int64_t ranges = block_overflow_ranges(limit, block_chunk_for(d->value_type));
+    const int64_t ranges = block_overflow_ranges(limit, block_chunk_for(d->value_type, limit));
     slots = align_up(static_cast<size_t>(ranges * 2 * 16) * w * sizeof(float), 256);
   }
   size_t total() const { return gather + vpart + slots; }

@@ -55,11 +55,10 @@ MFMA_PEAK_TFLOPS = {"fp16": 2500.0, "fp32": 157.3}
 FETCH_SCALE = 2.0
 WRITE_SCALE = 1.0
 PMC_KIB = {
-    (2, "csr", 128): {"fetch_kib": 216159.0 + 3876.9 + 245.5, "write_kib": 41413.3 + 659.8 + 16.4},
-    (3, "mixed", 128): {"fetch_kib": 124684.9 + 6310.1 + 169.7 + 131811.5 + 107.0,
-                        "write_kib": 22351.1 + 2266.5 + 8.1 + 14116.0 + 0.0},
+    (2, "csr", 128): {"fetch_kib": 210194.4 + 3876.9 + 245.7, "write_kib": 31379.3 + 659.8 + 16.4},
+    (3, "mixed", 128): {"fetch_kib": 122641.8 + 6310.1 + 169.6 + 131694.9 + 103.5,
+                        "write_kib": 12090.3 + 2266.5 + 8.1 + 14116.0 + 0.0},
 }
-
 
 def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
