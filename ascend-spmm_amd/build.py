@@ -30,6 +30,7 @@ HIP_SOURCES = [
     "spmm_gather.hip",
     "spmm_block.hip",
     "permute_rows.hip",
+    "spmm_cubeop.hip",
     "preprocess.hip",
 ]
 

@@ -119,7 +119,9 @@ struct MixedLayout {
   explicit MixedLayout(const spmm_mixed_desc* d) {
     const int64_t w = d->width > 0 ? d->width : 0;
     gather = align_up(gather_workspace_bytes(d->vector_nnz < 0 ? 0 : d->vector_nnz, w), 256);
-    const int64_t windows = d->block_windows > 0 ? d->block_windows : 0;
+    // vpart only when there is a vector part (rows of block windows may then
+    // have vector sums to hand over).
+    const int64_t windows = d->block_windows > 0 && d->vector_nnz > 0 ? d->block_windows : 0;
     vpart = align_up(static_cast<size_t>(16 * windows) * w * sizeof(float), 256);
     limit = d->block_count < d->block_values / 16 ? d->block_count : d->block_values / 16;
     if (limit < 0) limit = 0;
@@ -166,7 +168,7 @@ spmm_status spmm_mixed_run(const spmm_mixed_desc* d, const void* Crowptr, const 
     return fail(SPMM_ERR_CONTRACT, "spmm_ascend_cube: workspace too small: need " +
                                        std::to_string(lay.total()) + " bytes");
   char* ws = static_cast<char*>(workspace);
-  float* vpart = reinterpret_cast<float*>(ws + lay.gather);
+  float* vpart = lay.vpart > 0 ? reinterpret_cast<float*>(ws + lay.gather) : nullptr;
   float* slots = reinterpret_cast<float*>(ws + lay.gather + lay.vpart);
   // Vector pass first (it leaves the fp32 vector sums of block-window rows in
   // vpart), then the block part, which adds them and rounds once.

@@ -275,6 +275,47 @@ at::Tensor spmm_csr_aiv_mb_batch_impl(const at::Tensor& rowptr, const at::Tensor
   return spmm_csr_impl(rowptr, col, value, dense, start);
 }
 
+// spmm_cube, the legacy window-encoded operator (reference: spmm_cube_impl_npu,
+// extension/custom_op.cpp:91-113): rowptr indexes 16-row windows, col holds
+// (dense row << 4) | row in window.  Output [16 * windows, D].
+at::Tensor spmm_cube_impl(const at::Tensor& rowptr, const at::Tensor& col, const at::Tensor& value,
+                          const at::Tensor& dense, const at::Tensor& start) {
+  TORCH_CHECK_GPU(rowptr);
+  TORCH_CHECK_GPU(col);
+  TORCH_CHECK_GPU(value);
+  TORCH_CHECK_GPU(dense);
+  TORCH_CHECK_GPU(start);
+  TORCH_CHECK(rowptr.dim() == 1, "row must be a 1D Tensor, but got: ", rowptr.dim());
+  TORCH_CHECK(col.dim() == 1, "col must be a 1D Tensor, but got: ", col.dim());
+  TORCH_CHECK(value.dim() == 1, "value must be a 1D Tensor, but got: ", value.dim());
+  TORCH_CHECK(dense.dim() == 2, "dense must be a 2D Tensor, but got: ", dense.dim());
+  TORCH_CHECK(start.dim() == 1, "start must be a 1D Tensor, but got: ", start.dim());
+  check_dense_contract(dense, 16, "spmm_cube");
+  check_value_contract(value, dense, "value");
+  const int64_t nnz1 = col.size(0), nnz2 = value.size(0);
+  TORCH_CHECK(nnz1 == nnz2, "col and value must be same size, but got different: ", nnz1 - nnz2);
+  TORCH_CHECK(rowptr.size(0) >= 1, "row must hold at least one entry");
+  const int32_t it = index_type_of(rowptr, "rowptr");
+  TORCH_CHECK(index_type_of(col, "col") == it, "rowptr and col must have the same dtype");
+  check_same_device(rowptr, dense, "rowptr");
+  check_same_device(col, dense, "col");
+  check_same_device(value, dense, "value");
+
+  c10::DeviceGuard guard(dense.device());
+  const at::Tensor rp = rowptr.contiguous(), cl = col.contiguous();
+  const at::Tensor dn = aligned(dense);
+  const int64_t W = rowptr.size(0) - 1, D = dense.size(1);
+  auto result = at::empty({16 * W, D}, dense.options());
+  spmm_cube_op_desc d{W, nnz1, dense.size(0), D, it, value_type_of(dense)};
+  size_t ws_bytes = 0;
+  raise_status(spmm_cube_op_workspace(&d, &ws_bytes), "spmm_cube");
+  at::Tensor ws = workspace(dense, ws_bytes);
+  raise_status(spmm_cube_op_run(&d, rp.data_ptr(), cl.data_ptr(), value.data_ptr(), dn.data_ptr(),
+                                result.data_ptr(), ws.data_ptr(), ws_bytes, current_stream(dense)),
+               "spmm_cube");
+  return result;
+}
+
 // Row permutation helpers used by spmm_npu.pack_node_tensor / restore_node_tensor.
 at::Tensor pack_rows(const at::Tensor& tensor, const at::Tensor& inv, int64_t packed_rows) {
   TORCH_CHECK_GPU(tensor);
@@ -528,10 +569,10 @@ std::map<std::string, at::Tensor> preprocess(at::Tensor crow_ptr, at::Tensor col
   return finish(std::move(out), d);
 }
 
-// Schemas as in the reference (extension/custom_op.cpp:266-273); the
-// reference's spmm_cube legacy operator is not provided.
+// Schemas as in the reference (extension/custom_op.cpp:266-273).
 TORCH_LIBRARY(myops, m) {
   m.def("spmm_csr(Tensor rowptr, Tensor col, Tensor value, Tensor dense, Tensor start) -> Tensor");
+  m.def("spmm_cube(Tensor rowptr, Tensor col, Tensor value, Tensor dense, Tensor start) -> Tensor");
   m.def("spmm_ascend_cube(Tensor Crowptr, Tensor Ccol_ids, Tensor Cvalue, Tensor Vrowptr, Tensor Vcol_ids, Tensor Vvalue, Tensor dense, Tensor Cstart, Tensor Vstart) -> Tensor");
   m.def("spmm_csr_aiv_mb_batch(Tensor rowptr, Tensor col, Tensor value, Tensor dense, Tensor start) -> Tensor");
   m.def("spmm_ascend_cube_aic_without_pipeline(Tensor Crowptr, Tensor Ccol_ids, Tensor Cvalue, Tensor Vrowptr, Tensor Vcol_ids, Tensor Vvalue, Tensor dense, Tensor Cstart, Tensor Vstart) -> Tensor");
@@ -542,6 +583,7 @@ TORCH_LIBRARY(myops, m) {
 // extension/custom_op.cpp:276-283); on ROCm the GPU key is CUDA.
 TORCH_LIBRARY_IMPL(myops, CUDA, m) {
   m.impl("spmm_csr", &spmm_csr_impl);
+  m.impl("spmm_cube", &spmm_cube_impl);
   m.impl("spmm_ascend_cube", &spmm_ascend_cube_impl);
   m.impl("spmm_csr_aiv_mb_batch", &spmm_csr_aiv_mb_batch_impl);
   m.impl("spmm_ascend_cube_aic_without_pipeline", &spmm_ascend_cube_aic_without_pipeline_impl);
@@ -551,6 +593,8 @@ TORCH_LIBRARY_IMPL(myops, CUDA, m) {
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("spmm_csr", &spmm_csr_impl,
         "GPU CSR SpMM; FP16 width divisible by 16 with MAXD=1024, FP32 width divisible by 8 with MAXD=512");
+  m.def("spmm_cube", &spmm_cube_impl,
+        "GPU window-encoded SpMM (col = (dense row << 4) | row in window) on MFMA; width divisible by 16, MAXD=1024 for FP16 and 512 for FP32");
   m.def("spmm_ascend_cube", &spmm_ascend_cube_impl,
         "GPU mixed block(MFMA)/vector SpMM; width divisible by 16, MAXD=1024 for FP16 and 512 for FP32");
   m.def("spmm_ascend_cube_aic_without_pipeline", &spmm_ascend_cube_aic_without_pipeline_impl,

@@ -31,6 +31,7 @@ from custom_ops_lib import (  # noqa: E402
     spmm_ascend_cube_aiv_mb,
     spmm_csr,
     spmm_csr_aiv_mb_batch,
+    spmm_cube,
 )
 
 
@@ -110,4 +111,5 @@ __all__ = [
     "spmm_ascend_cube_aiv_mb",
     "spmm_csr",
     "spmm_csr_aiv_mb_batch",
+    "spmm_cube",
 ]

@@ -138,6 +138,39 @@ spmm_status spmm_mixed_run(const spmm_mixed_desc* desc,
 int64_t spmm_mixed_out_rows(const spmm_mixed_desc* desc);
 
 /* ------------------------------------------------------------------------
+ * spmm_cube_op — the legacy spmm_cube operator.  Window w (16 output rows)
+ * owns nonzeros [rowptr[w], rowptr[w+1]); each carries col = (c << 4) | r,
+ * c the dense row and r the row inside the window.  Maximal runs of
+ * consecutive nonzeros with equal c form one 16x1 block whose row r is the
+ * value of the run's last nonzero with row r:
+ *   out[16*w + r, :] = sum over window w's runs of block[r] * dense[c, :]
+ * with out rows = 16 * windows, every row written.  Replaces
+ * EXEC_NPU_CMD(aclnnSpmmCube, ...) in spmm_cube_impl_npu
+ * (extension/custom_op.cpp:91-113) and its kernel
+ * (kernels/op_kernel/spmm_cube.cpp:53-146).  Decoded on the device into the
+ * block layout of spmm_mixed_run and run on its MFMA block kernel.  c outside
+ * [0, dense_rows) contributes zero.  Width contract: 0 < N <= 1024 (fp16) or
+ * 512 (fp32), N % 16 == 0; dense and out 16-byte aligned; nnz < 2^31 - 1.
+ * The workspace holds the decoded blocks (16 values per nonzero at most).
+ * ---------------------------------------------------------------------- */
+typedef struct spmm_cube_op_desc {
+  int64_t windows;     /* rowptr.numel - 1                                */
+  int64_t nnz;         /* col.numel (== value.numel)                      */
+  int64_t dense_rows;  /* K                                               */
+  int64_t width;       /* N                                               */
+  int32_t index_type;
+  int32_t value_type;
+} spmm_cube_op_desc;
+
+spmm_status spmm_cube_op_workspace(const spmm_cube_op_desc* desc, size_t* bytes);
+
+spmm_status spmm_cube_op_run(const spmm_cube_op_desc* desc,
+                             const void* rowptr, const void* col, const void* value,
+                             const void* dense, void* out,
+                             void* workspace, size_t workspace_bytes,
+                             spmm_stream stream);
+
+/* ------------------------------------------------------------------------
  * Row permutation of a node tensor (P and P^T of the graph layout).
  *
  * spmm_pack_rows:    packed[inv[i], :] = src[i, :] for i < rows; every other

@@ -102,6 +102,44 @@ def spmm_f64(crow, col, values, dense) -> np.ndarray:
     return C
 
 
+def spmm_cube_f64(rowptr, col, values, dense) -> np.ndarray:
+    """The legacy spmm_cube operator in fp64 (kernels/op_kernel/spmm_cube.cpp:53-146):
+    rowptr indexes 16-row windows, col = (dense row << 4) | row in window;
+    runs of equal dense row form one 16x1 block, a later value of the same
+    row in a run replacing an earlier one.  Returns [16 * windows, N]."""
+    lib = _load()
+    rowptr = _i64(rowptr)
+    col = _i64(col)
+    val = np.ascontiguousarray(np.asarray(values, dtype=np.float64))
+    B = np.ascontiguousarray(np.asarray(dense, dtype=np.float64))
+    windows = rowptr.size - 1
+    K, N = B.shape
+    C = np.zeros((16 * windows, N), dtype=np.float64)
+    lib.or_spmm_cube_f64(ctypes.c_int64(windows), _p64(rowptr), _p64(col),
+                         val.ctypes.data_as(ctypes.POINTER(ctypes.c_double)), ctypes.c_int64(col.size),
+                         ctypes.c_int64(K), ctypes.c_int64(N),
+                         B.ctypes.data_as(ctypes.POINTER(ctypes.c_double)),
+                         C.ctypes.data_as(ctypes.POINTER(ctypes.c_double)))
+    return C
+
+
+def cube_encode(crow, col, values, nrows):
+    """Window-encoded form of a CSR matrix for spmm_cube: per 16-row window,
+    nonzeros ordered by (column, row) with col = (column << 4) | row.
+    Returns (rowptr[windows + 1], encoded col, values)."""
+    crow = _i64(crow)
+    col = _i64(col)
+    vals = np.asarray(values)
+    rows = np.repeat(np.arange(nrows, dtype=np.int64), np.diff(crow))
+    windows = (nrows + 15) // 16
+    order = np.lexsort((rows, col, rows // 16))
+    w = (rows // 16)[order]
+    rowptr = np.zeros(windows + 1, dtype=np.int64)
+    rowptr[1:] = np.cumsum(np.bincount(w, minlength=windows))
+    enc = (col[order] << 4) | (rows[order] & 15)
+    return rowptr, enc, vals[order]
+
+
 def cpu_reference(rows, cols, crow, col, values, dense):
     """The reference's CPU SpMM, ``cpu_reference``
     (tests/aic_aiv_ablation/common.py:173-177): torch CSR ``sparse.mm`` in

@@ -10,6 +10,8 @@
  *   or_spmm_f64         C = A*B in fp64 — the mathematics the kernels
  *                       (kernels/op_kernel/spmm_csr.cpp:383-423,
  *                       spmm_ascend_cube.cpp:16-311) approximate.
+ *   or_spmm_cube_f64    the window-encoded spmm_cube operator in fp64
+ *                       (kernels/op_kernel/spmm_cube.cpp:53-146)
  *   or_make_start       make_start (tests/task_mapping/common.py:119-127)
  *   or_csr_to_bcsr      ToBCSR (extension/custom_op.cpp:594-713)
  *   or_csr_to_cube      your_logic_kernel (extension/custom_op.cpp:429-560)
@@ -61,6 +63,46 @@ void or_spmm_f64(int64_t rows, const int64_t* rowptr, const int64_t* col, const 
       const double v = val[p];
       const double* b = B + c * N;
       for (int64_t n = 0; n < N; ++n) out[n] += v * b[n];
+    }
+  }
+}
+
+/* Window-encoded SpMM of the legacy spmm_cube operator
+ * (kernels/op_kernel/spmm_cube.cpp:53-146): window w owns nonzeros
+ * [rowptr[w], rowptr[w+1]); col = (c << 4) | r.  A maximal run of
+ * consecutive nonzeros with equal c is one 16x1 block whose row r holds the
+ * value of the run's last nonzero with row r (the kernel stores each value
+ * into its block slot, so a later one overwrites); the block adds
+ * block[r] * B[c, :] to output row 16*w + r.  c outside [0, K) adds nothing.
+ * Output: 16 * windows rows, in fp64. */
+void or_spmm_cube_f64(int64_t windows, const int64_t* rowptr, const int64_t* col, const double* val,
+                      int64_t nnz, int64_t K, int64_t N, const double* B, double* C) {
+  for (int64_t i = 0; i < 16 * windows * N; ++i) C[i] = 0.0;
+  for (int64_t w = 0; w < windows; ++w) {
+    int64_t a = rowptr[w], b = rowptr[w + 1];
+    a = a < 0 ? 0 : (a > nnz ? nnz : a);
+    b = b < a ? a : (b > nnz ? nnz : b);
+    int64_t p = a;
+    while (p < b) {
+      const int64_t c = col[p] >> 4;
+      double blk[16];
+      int have[16];
+      for (int r = 0; r < 16; ++r) { blk[r] = 0.0; have[r] = 0; }
+      int64_t q = p;
+      while (q < b && (col[q] >> 4) == c) {
+        const int r = (int)(col[q] & 15);
+        blk[r] = val[q];
+        have[r] = 1;
+        ++q;
+      }
+      if (c >= 0 && c < K)
+        for (int r = 0; r < 16; ++r)
+          if (have[r]) {
+            double* out = C + (16 * w + r) * N;
+            const double* row = B + c * N;
+            for (int64_t n = 0; n < N; ++n) out[n] += blk[r] * row[n];
+          }
+      p = q;
     }
   }
 }

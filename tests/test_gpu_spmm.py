@@ -298,3 +298,67 @@ def test_config2_full_size_matches_oracle(spmm_npu):
     B = w.dense(128)
     out = run_csr(spmm_npu, w.crow, w.col, w.values, B)
     assert_close(out, O.spmm_f64(w.crow, w.col, w.values, B), "fp16")
+
+
+# ------------------------------------------------------------- spmm_cube
+
+@pytest.mark.parametrize("dtype", ["fp16", "fp32"])
+@pytest.mark.parametrize("width", [16, 128, 512])
+@pytest.mark.parametrize("index_dtype", [torch.int32, torch.int64])
+def test_spmm_cube_matches_oracle(spmm_npu, dtype, width, index_dtype):
+    rng = np.random.default_rng(40 + width)
+    n, K = 300, 257
+    crow, col = random_csr(rng, n, K, 20, long_rows=[(5, 200), (17, 250)])
+    val = rng.uniform(-1, 1, col.size).astype(NP_DT[dtype])
+    B = rng.standard_normal((K, width)).astype(NP_DT[dtype])
+    rp, enc, v = O.cube_encode(crow, col, val, n)
+    out = spmm_npu.spmm_cube(dev(rp, index_dtype), dev(enc, index_dtype), dev(v), dev(B), zero_start(20))
+    assert out.shape == (16 * (rp.size - 1), width) and out.dtype == dev(B).dtype
+    ref = O.spmm_cube_f64(rp, enc, v, B)
+    tol = TOL[dtype]
+    np.testing.assert_allclose(out.double().cpu().numpy(), ref, atol=tol, rtol=tol)
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "fp32"])
+def test_spmm_cube_equals_bcsr_block_part_bitwise(spmm_npu, dtype):
+    """Encoded runs are the BCSR(16x1) blocks of csr_to_bcsr in the same
+    order, so spmm_cube and spmm_ascend_cube on the BCSR run the same MFMA
+    sequence."""
+    rng = np.random.default_rng(9)
+    n, K, width = 400, 600, 64
+    crow, col = random_csr(rng, n, K, 30)
+    val = rng.uniform(-1, 1, col.size).astype(NP_DT[dtype])
+    B = rng.standard_normal((K, width)).astype(NP_DT[dtype])
+    rp, enc, v = O.cube_encode(crow, col, val, n)
+    cube = spmm_npu.spmm_cube(dev(rp, torch.int32), dev(enc, torch.int32), dev(v), dev(B), zero_start(20))
+    b = O.csr_to_bcsr(crow, col, val, n, K, 16)
+    i32 = torch.int32
+    block = spmm_npu.spmm_ascend_cube(dev(b["crow_window_ptr"], i32), dev(b["unique_col_ids"], i32),
+                                      dev(b["value"]), dev(np.zeros(1, np.int32)),
+                                      torch.zeros(0, dtype=i32, device="cuda"),
+                                      torch.zeros(0, dtype=dev(v).dtype, device="cuda"), dev(B),
+                                      zero_start(20), zero_start(40))
+    assert torch.equal(cube, block)
+
+
+def test_spmm_cube_runs_overwrites_and_edges(spmm_npu):
+    rowptr = np.array([0, 6, 6, 7], np.int64)
+    col = np.array([(2 << 4) | 0, (2 << 4) | 0, (2 << 4) | 3, (1 << 4) | 1, (2 << 4) | 1, (9 << 4) | 2,
+                    (0 << 4) | 15], np.int64)
+    val = np.array([1.0, 5.0, 4.0, 2.0, 7.0, 100.0, 3.0], np.float32)
+    B = np.tile(np.array([[1.0], [2.0], [3.0], [4.0]], np.float32), (1, 16))
+    out = spmm_npu.spmm_cube(dev(rowptr), dev(col), dev(val), dev(B), zero_start(20))
+    np.testing.assert_array_equal(out.cpu().numpy(), O.spmm_cube_f64(rowptr, col, val, B).astype(np.float32))
+    # no nonzeros: all windows zero
+    empty = spmm_npu.spmm_cube(dev(np.zeros(4, np.int64)), dev(np.zeros(0, np.int64)),
+                               dev(np.zeros(0, np.float16)), dev(np.ones((5, 32), np.float16)), zero_start(20))
+    assert empty.shape == (48, 32) and not empty.any()
+
+
+def test_spmm_cube_contract_errors(spmm_npu):
+    rp = dev(np.array([0, 1], np.int32))
+    c = dev(np.array([0], np.int32))
+    with pytest.raises(RuntimeError, match="spmm_cube requires feature width divisible by 16"):
+        spmm_npu.spmm_cube(rp, c, dev(np.ones(1, np.float32)), dev(np.ones((2, 8), np.float32)), zero_start(20))
+    with pytest.raises(RuntimeError, match="col and value must be same size"):
+        spmm_npu.spmm_cube(rp, c, dev(np.ones(2, np.float16)), dev(np.ones((2, 16), np.float16)), zero_start(20))

@@ -27,9 +27,9 @@ def test_surface_matches_reference_module(api):
     for name in ("spmm_csr", "spmm_ascend_cube", "csr_to_bcsr", "csr_to_ascend_cube", "preprocess",
                  "block_level_split", "pack_node_tensor", "restore_node_tensor",
                  "spmm_ascend_cube_aic_without_pipeline", "spmm_ascend_cube_aiv_mb",
-                 "spmm_csr_aiv_mb_batch", "make_start"):
+                 "spmm_csr_aiv_mb_batch", "spmm_cube", "make_start"):
         assert callable(getattr(api, name)), name
-    for op in ("spmm_csr", "spmm_ascend_cube", "spmm_csr_aiv_mb_batch",
+    for op in ("spmm_csr", "spmm_cube", "spmm_ascend_cube", "spmm_csr_aiv_mb_batch",
                "spmm_ascend_cube_aic_without_pipeline", "spmm_ascend_cube_aiv_mb"):
         assert hasattr(torch.ops.myops, op), op
 

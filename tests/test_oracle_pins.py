@@ -543,3 +543,38 @@ def test_pack_restore_closed_form():
     assert not packed[np.setdiff1d(np.arange(32), inv)].any()
     np.testing.assert_array_equal(O.restore_node_tensor(packed, inv), x)
     assert O.pack_node_tensor(x, inv).shape[0] == inv.max() + 1
+
+
+# ------------------------------------------------------------- spmm_cube
+
+def test_spmm_cube_closed_form_on_encoded_csr():
+    """A CSR matrix encoded window by window (column-major within a window)
+    gives exactly A @ B: every run is one distinct (window, column) block."""
+    rng = np.random.default_rng(21)
+    for n, K, N in ((45, 30, 8), (16, 5, 4), (70, 200, 16)):
+        crow, col = rand_csr(rng, n, K, 9)
+        val = rng.standard_normal(col.size)
+        B = rng.standard_normal((K, N))
+        rp, enc, v = O.cube_encode(crow, col, val, n)
+        assert rp.size == (n + 15) // 16 + 1 and rp[-1] == col.size
+        C = O.spmm_cube_f64(rp, enc, v, B)
+        np.testing.assert_allclose(C[:n], dense_of(crow, col, val, n, K) @ B, rtol=1e-12, atol=1e-12)
+        assert not C[n:].any()
+
+
+def test_spmm_cube_known_answer_runs_and_overwrites():
+    # window 0: run c=2 {r0: 1, r0: 5 (replaces 1), r3: 4}, run c=1 {r1: 2},
+    # run c=2 again {r1: 7} (a new block: adds), c=9 >= K ignored;
+    # window 1 empty; window 2: c=0 {r15: 3}.
+    rowptr = np.array([0, 6, 6, 7], np.int64)
+    col = np.array([(2 << 4) | 0, (2 << 4) | 0, (2 << 4) | 3, (1 << 4) | 1, (2 << 4) | 1, (9 << 4) | 2,
+                    (0 << 4) | 15], np.int64)
+    val = np.array([1.0, 5.0, 4.0, 2.0, 7.0, 100.0, 3.0])
+    B = np.array([[1.0, 10.0], [2.0, 20.0], [3.0, 30.0], [4.0, 40.0]])  # K = 4
+    C = O.spmm_cube_f64(rowptr, col, val, B)
+    want = np.zeros((48, 2))
+    want[0] = 5 * B[2]
+    want[3] = 4 * B[2]
+    want[1] = 2 * B[1] + 7 * B[2]
+    want[32 + 15] = 3 * B[0]
+    np.testing.assert_array_equal(C, want)
