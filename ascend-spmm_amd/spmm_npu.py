@@ -55,6 +55,36 @@ def make_start(pointer, cores):
     return idx.clamp_min(0).to(torch.int32)
 
 
+class _PackRows(torch.autograd.Function):
+    """packed[inv[i]] = x[i] (HIP scatter); backward gathers grad[inv[i]]."""
+
+    @staticmethod
+    def forward(ctx, tensor, index, packed_rows):
+        ctx.save_for_backward(index)
+        return _pack_rows(tensor, index, packed_rows)
+
+    @staticmethod
+    def backward(ctx, grad):
+        (index,) = ctx.saved_tensors
+        return _restore_rows(grad.contiguous(), index), None, None
+
+
+class _RestoreRows(torch.autograd.Function):
+    """out[i] = packed[inv[i]] (HIP gather); backward scatters into a zero
+    tensor of the packed shape (inv is a permutation: no two i share a row)."""
+
+    @staticmethod
+    def forward(ctx, packed, index):
+        ctx.save_for_backward(index)
+        ctx.packed_rows = packed.size(0)
+        return _restore_rows(packed, index)
+
+    @staticmethod
+    def backward(ctx, grad):
+        (index,) = ctx.saved_tensors
+        return _pack_rows(grad.contiguous(), index, ctx.packed_rows), None
+
+
 def pack_node_tensor(tensor, inv_permutation, packed_rows=None):
     """Apply ``P`` once to a tensor whose leading dimension is original node id.
 
@@ -78,7 +108,7 @@ def pack_node_tensor(tensor, inv_permutation, packed_rows=None):
         packed_rows = int(packed_rows)
     if packed_rows < minimum_rows:
         raise ValueError("packed_rows is smaller than the permutation extent")
-    return _pack_rows(tensor, index.contiguous(), packed_rows)
+    return _PackRows.apply(tensor, index.contiguous(), packed_rows)
 
 
 def restore_node_tensor(packed_tensor, inv_permutation):
@@ -95,10 +125,79 @@ def restore_node_tensor(packed_tensor, inv_permutation):
         or int(index.max().item()) >= packed_tensor.size(0)
     ):
         raise ValueError("inv_permutation contains an invalid packed node id")
-    return _restore_rows(packed_tensor, index.contiguous())
+    return _RestoreRows.apply(packed_tensor, index.contiguous())
+
+
+class _PackedGraphSpMM(torch.autograd.Function):
+    """Y_p = (P A P^T) X_p on the mixed operator; dX_p = (P A^T P^T) dY_p on
+    the same operator with the fixed-layout transpose split."""
+
+    @staticmethod
+    def forward(ctx, graph, x_packed):
+        ctx.graph = graph
+        return spmm_ascend_cube(*graph.forward_ops, x_packed, graph.cstart, graph.vstart)
+
+    @staticmethod
+    def backward(ctx, grad):
+        g = ctx.graph
+        return None, spmm_ascend_cube(*g.transpose_ops, grad.contiguous(), g.tcstart, g.tvstart)
+
+
+class PackedGraph:
+    """A fixed square graph in the packed layout of
+    ``preprocess(..., graph_layout=True)``, as a differentiable operator on
+    packed node tensors.
+
+    ``graph(x_packed)`` returns ``P A P^T x_packed`` (``spmm_ascend_cube`` on
+    the renumbered block and vector parts).  Its backward multiplies by
+    ``P A^T P^T``: ``spmm_ascend_cube`` on the ``transpose_*`` keys, the
+    fixed-layout split of the packed transpose that the reference computes
+    (extension/custom_op.cpp:1072-1078, 1350-1384) but never consumes.
+    Gradients flow to the node tensor only (the graph is constant).  Compose
+    with ``pack_node_tensor`` / ``restore_node_tensor``, which are
+    differentiable too.
+    """
+
+    def __init__(self, prep, device=None):
+        if "transpose_crow_window_ptr" not in prep or int(prep["packed_layout_supported"][0]) == 0:
+            raise ValueError("PackedGraph needs preprocess(..., graph_layout=True) on a square matrix")
+        dev = torch.device(device) if device is not None else prep["crow_window_ptr"].device
+        if dev.type == "cpu":
+            dev = torch.device("cuda", torch.cuda.current_device())
+        i32 = torch.int32
+
+        def ix(t):
+            return t.to(device=dev, dtype=i32).contiguous()
+
+        def vx(t):
+            return t.to(device=dev).contiguous()
+
+        self.packed_rows = int(prep["packed_rows"][0].item())
+        self.inv_permutation = prep["inv_permutation"].to(dev)
+        self.forward_ops = (ix(prep["crow_window_ptr"]), ix(prep["renumbered_unique_col_ids"]), vx(prep["value"]),
+                            ix(prep["vrow_window_ptr"]), ix(prep["renumbered_vcol_indices"]), vx(prep["vvalue"]))
+        self.transpose_ops = (ix(prep["transpose_crow_window_ptr"]), ix(prep["transpose_unique_col_ids"]),
+                              vx(prep["transpose_value"]), ix(prep["transpose_vrow_window_ptr"]),
+                              ix(prep["transpose_vcol_indices"]), vx(prep["transpose_vvalue"]))
+        self.cstart = make_start(prep["crow_window_ptr"], 20).to(dev)
+        self.vstart = make_start(prep["vrow_window_ptr"], 40).to(dev)
+        self.tcstart = make_start(prep["transpose_crow_window_ptr"], 20).to(dev)
+        self.tvstart = make_start(prep["transpose_vrow_window_ptr"], 40).to(dev)
+
+    def __call__(self, x_packed):
+        if x_packed.size(0) != self.packed_rows:
+            raise ValueError("x_packed must have packed_rows rows")
+        return _PackedGraphSpMM.apply(self, x_packed)
+
+    def pack(self, x):
+        return pack_node_tensor(x, self.inv_permutation, self.packed_rows)
+
+    def restore(self, y_packed):
+        return restore_node_tensor(y_packed, self.inv_permutation)
 
 
 __all__ = [
+    "PackedGraph",
     "block_level_split",
     "csr_to_ascend_cube",
     "csr_to_bcsr",
