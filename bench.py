@@ -341,6 +341,8 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": traffic,
+            "traffic_gbps": None if traffic is None else round(traffic / (event_ms / 1e3) / 1e9, 1),
+            "traffic_frac": None if traffic is None else round(traffic / (event_ms / 1e3) / 1e9 / HBM_PEAK_GBPS, 4),
             "algorithmic_bytes_per_call": alg_bytes,
             "gather_model_bytes": int(w.nnz * width * s_b),
             "event_ms_per_call": round(event_ms, 5),
