@@ -38,6 +38,15 @@
 #include "common.h"
 #include "lanevec.h"
 
+#include <type_traits>
+
+// Raw buffer load of 16 bytes (the LLVM AMDGPU intrinsic): address = the
+// resource's base + voffset + soffset, with the resource's range check
+// (a load whose offset is past the extent returns zeros).
+typedef int spmm_rsrc_t __attribute__((ext_vector_type(4)));
+__device__ spmm::lanes::raw16_t spmm_raw_buffer_load_b128(spmm_rsrc_t rsrc, uint32_t voffset, uint32_t soffset,
+                                                          int32_t aux) __asm("llvm.amdgcn.raw.buffer.load.v4i32");
+
 namespace spmm {
 namespace {
 
@@ -49,10 +58,6 @@ constexpr int kWgThreads = 256;
 #define SPMM_GATHER_BATCH 4
 #endif
 constexpr int kBatch = SPMM_GATHER_BATCH;  // dense rows per batch
-#ifndef SPMM_GATHER_INFLIGHT
-#define SPMM_GATHER_INFLIGHT 2
-#endif
-constexpr int kInFlight = SPMM_GATHER_INFLIGHT;  // batches in flight per lane group
 constexpr int kStageUnroll = 8;             // staging loads issued per thread before storing
 // A row is "short" (summed by one lane group, never split) when it holds at
 // most R / SPMM_GATHER_SHORT_DIV nonzeros.
@@ -72,7 +77,6 @@ template <typename I>
 struct Geometry {
   const I* rowptr;
   int64_t* tail;           // [nranges]: row that starts in range j and runs past its end, or -1
-  int64_t* tile_row;       // [tiles + 1]: row holding the first position of tile t
   int64_t row_lo, row_hi;  // rows handled
   int64_t vrows;           // rowptr holds vrows + 1 entries; rows >= vrows are empty
   int64_t nnz;             // extent of col[] / value[]
@@ -104,19 +108,50 @@ struct Geometry {
   }
 };
 
-// LDS entry of one staged nonzero (16 bytes, read with one ds_read_b128):
-//   x: column id, or kBadCol when it is outside [0, K)
-//   y: value bits (fp16 zero-extended, or fp32)
-//   z: row mark, (row + 1 - rS) << 2 | to_vpart << 1 | ends_here, where the
-//      row part is set only at the position a row starts
+// A staged tile is three LDS arrays over its positions (structure of arrays,
+// 8 + sizeof(T) bytes per position; 4 aligned positions are read with one
+// load of each array):
+//   src:  where the position's dense row is read from (see the loaders)
+//   mark: 0, or at the last position of a row (row + 1 - rS) << 1 | to_vpart
+//   val:  value bits (the value type's own width); -0 for an invalid column
 constexpr uint32_t kBadCol = 0xFFFFFFFFu;
+static_assert(kBatch % 4 == 0 && (kBatch & (kBatch - 1)) == 0, "batches are read 4 positions at a time");
 
 template <typename T>
-__device__ inline uint32_t value_bits(T v) {
-  if constexpr (sizeof(T) == 2)
-    return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, v));
-  else
-    return __builtin_bit_cast(uint32_t, v);
+using ValBits = typename std::conditional<sizeof(T) == 2, uint16_t, uint32_t>::type;
+template <typename T>
+constexpr ValBits<T> kNegZero = sizeof(T) == 2 ? 0x8000u : 0x80000000u;
+
+template <typename T>
+struct Staged {
+  uint32_t* src;
+  uint32_t* mark;
+  ValBits<T>* val;
+  __device__ inline Staged(unsigned char* smem, int64_t positions)
+      : src(reinterpret_cast<uint32_t*>(smem)),
+        mark(reinterpret_cast<uint32_t*>(smem) + positions),
+        val(reinterpret_cast<ValBits<T>*>(reinterpret_cast<uint32_t*>(smem) + 2 * positions)) {}
+  static constexpr size_t bytes_per_position() { return 8 + sizeof(ValBits<T>); }
+  // Value bits of 4 consecutive positions from p (p % 4 == 0).
+  __device__ inline void values4(int32_t p, uint32_t* vb) const {
+    if constexpr (sizeof(T) == 2) {
+      typedef unsigned int u2 __attribute__((ext_vector_type(2)));
+      const u2 r = *reinterpret_cast<const u2*>(val + p);
+      vb[0] = r[0] & 0xFFFFu;
+      vb[1] = r[0] >> 16;
+      vb[2] = r[1] & 0xFFFFu;
+      vb[3] = r[1] >> 16;
+    } else {
+      const lanes::raw16_t r = *reinterpret_cast<const lanes::raw16_t*>(val + p);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) vb[u] = r[u];
+    }
+  }
+};
+
+template <typename T>
+__device__ inline ValBits<T> value_bits(T v) {
+  return __builtin_bit_cast(ValBits<T>, v);
 }
 template <typename T>
 __device__ inline float bits_value(uint32_t b) {
@@ -126,112 +161,191 @@ __device__ inline float bits_value(uint32_t b) {
     return __builtin_bit_cast(float, b);
 }
 
-// One batch of kBatch consecutive nonzeros: raw 16-byte dense pieces, values
-// and row marks.  Positions past the range end or with an invalid column
-// carry value -0 and a zero dense piece, so their FMA adds exactly -0 (the
-// identity of fp32 addition); positions past the range end carry mark 0.
+// Dense-row loaders.  Each stages a 32-bit source per position and turns it
+// into the lane's 16 bytes of that dense row, or zeros for an invalid column
+// (whose staged value is -0, so the FMA adds exactly -0: the identity of
+// fp32 addition, as an accumulator is never -0).
+//
+// BufferLoader (dense operands up to kBufferLimit bytes): the source is the
+// row's byte offset col * row_bytes, read with a raw buffer load whose extent
+// is the dense operand; an invalid column stages kBufferNone, which with any
+// lane offset (< 4096) lies past the extent, so the buffer range check
+// returns zeros without a memory access.  No address arithmetic per position.
+constexpr uint32_t kBufferNone = 0xFFFFF000u;
+constexpr int64_t kBufferLimit = kBufferNone;
+
+using ::spmm_rsrc_t;
+using ::spmm_raw_buffer_load_b128;
+
+template <typename T>
+struct BufferLoader {
+  spmm_rsrc_t rsrc;
+  uint32_t lane_bytes;  // c0 * sizeof(T)
+  static constexpr uint32_t kNone = kBufferNone;
+  __device__ inline BufferLoader(const T* dense, int64_t K, int64_t N, int64_t c0) {
+    const uint64_t a = reinterpret_cast<uint64_t>(dense);
+    rsrc[0] = static_cast<int>(a & 0xFFFFFFFFu);
+    rsrc[1] = static_cast<int>((a >> 32) & 0xFFFFu);  // stride 0: raw buffer
+    rsrc[2] = static_cast<int>(static_cast<uint32_t>(K * N * static_cast<int64_t>(sizeof(T))));
+    rsrc[3] = 0x00020000;  // 32-bit data format; no swizzle, no thread-id offset
+    lane_bytes = static_cast<uint32_t>(c0 * static_cast<int64_t>(sizeof(T)));
+  }
+  __device__ static inline uint32_t stage(int64_t c, int64_t K, int64_t N) {
+    return static_cast<uint64_t>(c) < static_cast<uint64_t>(K)
+               ? static_cast<uint32_t>(c) * static_cast<uint32_t>(N * static_cast<int64_t>(sizeof(T)))
+               : kNone;
+  }
+  __device__ inline lanes::raw16_t load(uint32_t src) const {
+    return spmm_raw_buffer_load_b128(rsrc, src + lane_bytes, 0u, 0);
+  }
+};
+
+// GlobalLoader (larger dense operands): the source is the column id, or
+// kBadCol; invalid columns load dense row 0 (K >= 1 here) and use zeros.
+template <typename T>
+struct GlobalLoader {
+  const T* dense_c0;  // dense + c0
+  uint32_t N;
+  static constexpr uint32_t kNone = kBadCol;
+  __device__ inline GlobalLoader(const T* dense, int64_t, int64_t n, int64_t c0)
+      : dense_c0(dense + c0), N(static_cast<uint32_t>(n)) {}
+  __device__ static inline uint32_t stage(int64_t c, int64_t K, int64_t) {
+    return static_cast<uint64_t>(c) < static_cast<uint64_t>(K) ? static_cast<uint32_t>(c) : kNone;
+  }
+  __device__ inline lanes::raw16_t load(uint32_t src) const {
+    const bool ok = src != kNone;
+    const lanes::raw16_t x = lanes::load_raw16(dense_c0 + static_cast<uint64_t>(ok ? src : 0u) * N);
+    const lanes::raw16_t zero = {0u, 0u, 0u, 0u};
+    return ok ? x : zero;
+  }
+};
+
+// One batch of kBatch consecutive positions: the lanes' 16-byte dense
+// pieces, values and row-end marks.  Positions outside [ps, pe) carry source
+// kNone (zero piece), value -0 and mark 0.
 template <typename T>
 struct Batch {
   lanes::raw16_t x[kBatch];
   float v[kBatch];
-  int32_t m[kBatch];
-  uint32_t ok;  // bit u: position u has a dense piece to use
+  uint32_t m[kBatch];
 };
 
-// Issues the dense loads of a batch from the LDS entries.  Positions are
-// relative to the tile start.  Branch-free so the loads of a batch stay in
-// flight together: skipped positions load dense row 0 (K >= 1 here).
-template <typename T>
+// Issues the dense loads of a batch from the staged arrays.  Positions are
+// relative to the tile start; a batch starts at a multiple of 4.  The
+// unmasked form is for batches wholly inside [ps, pe); the masked form (a
+// range's first and last batches) gives positions outside it source kNone,
+// value -0 and mark 0.
+template <typename T, typename Loader>
 struct Stream {
-  const lanes::raw16_t* s_ent;
-  const T* dense_c0;  // dense + c0
-  uint32_t N;
-  int32_t pe;
+  Staged<T> s;
+  Loader ld;
+  int32_t ps, pe;
 
+  template <bool kMasked>
   __device__ inline void issue(Batch<T>& b, int32_t p0) const {
-    b.ok = 0;
 #pragma unroll
-    for (int u = 0; u < kBatch; ++u) {
-      const int32_t p = p0 + u;
-      const bool in = p < pe;
-      const lanes::raw16_t e = s_ent[in ? p : pe - 1];
-      const bool ok = in && e.x != kBadCol;
-      b.ok |= ok ? 1u << u : 0u;
-      b.v[u] = ok ? bits_value<T>(e.y) : -0.0f;
-      b.m[u] = in ? static_cast<int32_t>(e.z) : 0;
-      const uint64_t off = static_cast<uint64_t>(ok ? e.x : 0u) * N;
-      b.x[u] = lanes::load_raw16(dense_c0 + off);
+    for (int q = 0; q < kBatch; q += 4) {
+      // A masked batch reads no aligned group past the one holding pe - 1.
+      const int32_t pq = !kMasked || p0 + q < pe ? p0 + q : ((pe - 1) & ~3);
+      const lanes::raw16_t c4 = *reinterpret_cast<const lanes::raw16_t*>(s.src + pq);
+      const lanes::raw16_t m4 = *reinterpret_cast<const lanes::raw16_t*>(s.mark + pq);
+      uint32_t vb[4];
+      s.values4(pq, vb);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int32_t p = p0 + q + u;
+        const bool in = !kMasked || (p >= ps && p < pe);
+        b.v[q + u] = bits_value<T>(in ? vb[u] : static_cast<uint32_t>(kNegZero<T>));
+        b.m[q + u] = in ? m4[u] : 0u;
+        b.x[q + u] = ld.load(in ? c4[u] : Loader::kNone);
+      }
     }
   }
 };
 
-// Accumulates batches in position order: tracks the current row from the
-// marks, routes rows of block windows to vpart, and flushes at row ends.
+// Accumulates batches in position order and flushes at row ends: rows of
+// block windows go to vpart, the first row of a range that began before the
+// range goes to the head slot, and the rest are rounded into out.
 template <typename T>
 struct Sink {
-  const lanes::raw16_t* s_ent;
   int64_t rS, row_hi;
   T* out;
   int64_t N, c0;
   float* vpart;
   float* head_slot;
   float* tail_slot;
-  int32_t rel;             // row in progress + 1 - rS; 0 while it is one started before the range
-  bool to_vpart;           // the row in progress belongs to a block window
+  bool head;  // the row in progress began before this range
   float acc[lanes::LaneVec<T>::V];
 
-  __device__ inline void flush() {
+  __device__ inline void flush(uint32_t m) {
     constexpr int V = lanes::LaneVec<T>::V;
-    const int64_t row = rS + rel - 1;
-    // fp32 destinations: the head slot (row begun before the range) and
-    // vpart (block-window rows); others are rounded into out.
+    const int64_t row = rS + static_cast<int64_t>(m >> 1) - 1;
     if (row < row_hi) {
-      if (rel == 0 || to_vpart) {
-        float* dst = rel == 0 ? head_slot : vpart + row * N + c0;
+      if (head || (m & 1u)) {
+        float* dst = head ? head_slot : vpart + row * N + c0;
 #pragma unroll
         for (int i = 0; i < V; ++i) dst[i] = acc[i];
       } else {
         lanes::LaneVec<T>::store(out + row * N + c0, acc);
       }
     }
+    head = false;
 #pragma unroll
     for (int i = 0; i < V; ++i) acc[i] = 0.f;
   }
 
   __device__ inline void consume(const Batch<T>& b) {
     constexpr int V = lanes::LaneVec<T>::V;
-    const lanes::raw16_t zero = {0u, 0u, 0u, 0u};
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
-      const int32_t m = b.m[u];
-      const int32_t start = m >> 2;
-      rel = start ? start : rel;
-      to_vpart = start ? (m & 2) != 0 : to_vpart;
       float x[V];
-      lanes::LaneVec<T>::unpack((b.ok >> u & 1u) ? b.x[u] : zero, x);
+      lanes::LaneVec<T>::unpack(b.x[u], x);
 #pragma unroll
       for (int i = 0; i < V; ++i) acc[i] = __builtin_fmaf(b.v[u], x[i], acc[i]);
-      if (m & 1) flush();
+      if (b.m[u] != 0u) flush(b.m[u]);
     }
   }
 
   // The row in progress at the range end continues into the next range:
-  // returns that row if it started in this range (a tail), else -1.
-  __device__ inline int64_t finish(int32_t pe) {
+  // its partial goes to the head slot if it began before the range, else to
+  // the tail slot, and `crossing` (the long row crossing the range end) is
+  // returned as the range's tail row.  Returns -1 when no row is open.
+  __device__ inline int64_t finish(bool open, int64_t crossing) {
     constexpr int V = lanes::LaneVec<T>::V;
-    if (s_ent[pe - 1].z & 1u) return -1;
-    float* dst = rel == 0 ? head_slot : tail_slot;
+    if (!open) return -1;
+    float* dst = head ? head_slot : tail_slot;
 #pragma unroll
     for (int i = 0; i < V; ++i) dst[i] = acc[i];
-    return rel == 0 ? -1 : rS + rel - 1;
+    return head ? -1 : crossing;
   }
 };
+
+// Row holding position P (rp(row_lo) <= P < rp(row_hi)): a multiway search
+// over rowptr by one wavefront.  Each round keeps a bracket [lo, hi) with
+// rp(lo) <= P < rp(hi) and probes one row per active lane, evenly spaced
+// inside it (lo + step, lo + 2*step, ...); the probes at or below P form a
+// prefix, whose length moves lo.  A full wavefront needs ceil(log65(rows))
+// rounds; the result is uniform across the wavefront.
+template <typename I>
+__device__ inline int64_t find_row(const Geometry<I>& g, int64_t P) {
+  const int lane = static_cast<int>(threadIdx.x & 63);
+  const int lanes = __popcll(__ballot(true));  // a work-group's last wavefront may be partial
+  int64_t lo = g.row_lo, hi = g.row_hi;
+  while (hi - lo > 1) {
+    const int64_t step = (hi - lo + lanes) / (lanes + 1);
+    const int64_t r = lo + (lane + 1) * step;
+    const bool le = r < hi && g.rp(r) <= P;
+    lo += __popcll(__ballot(le)) * step;
+    hi = lo + step < hi ? lo + step : hi;
+  }
+  return lo;
+}
 
 #ifndef SPMM_GATHER_WAVES
 #define SPMM_GATHER_WAVES 5
 #endif
 // Waves per SIMD the register budget of gather_tiles is fitted to.
-template <typename T, typename I>
+template <typename T, typename I, typename Loader>
 __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM_GATHER_WAVES))) void gather_tiles(
     Geometry<I> g, const I* __restrict__ col, const T* __restrict__ value,
     const T* __restrict__ dense, int64_t K, int64_t N, T* __restrict__ out, float* __restrict__ ws,
@@ -241,11 +355,12 @@ __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM
   // The tile's positions plus a halo of one range: a short row that starts
   // in the tile's last range is finished from the halo.
   const int64_t tile_positions = (ranges_per_tile + 1) * g.range;
-  lanes::raw16_t* s_ent = reinterpret_cast<lanes::raw16_t*>(smem);
-  uint32_t* s_word = reinterpret_cast<uint32_t*>(smem);  // s_word[4*i + 2] = mark of entry i
-  // s_cut[k]: end (relative to P0) of the short row crossing the tile's k-th
-  // range boundary P0 + k*R, or -1.
+  const Staged<T> sa(smem, tile_positions);
+  // Per range boundary k of the tile (position P0 + k*R, k = 0..ranges):
+  //  s_cut[k]:  end (relative to P0) of the short row crossing it, or -1;
+  //  s_long[k]: the long row crossing it, or -1.
   __shared__ int32_t s_cut[kTileRanges + 1];
+  __shared__ int64_t s_long[kTileRanges + 1];
 
   // wg_split > 1: the tile's column chunks go to wg_split work-groups (chunk
   // = blockIdx % wg_split); consecutive blockIdx land on different XCDs, so
@@ -257,20 +372,20 @@ __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM
   const int64_t P0 = g.lo(j0), P1 = g.hi(j1 - 1);
   const int64_t base = g.rp(g.row_lo), end = g.rp(g.row_hi);
 
-  // Rows overlapping the tile: [rS, rE) with rS = the row holding position P0
-  // and rE = one past the row holding P1 (the next tile's first position),
-  // from the tile-row table of gather_tile_rows; tiles starting outside our
-  // positions [base, end) clamp to the row range.  Runs of empty rows before
-  // the tile are skipped.
-  const int64_t rS = P0 < base ? g.row_lo : (P0 < end ? g.tile_row[tile] : g.row_hi);
-  const int64_t rE = P1 < base ? g.row_lo : (P1 < end ? g.tile_row[tile + 1] + 1 : g.row_hi);
-
-  // Stage the tile's nonzeros as LDS entries (positions clamped to [0, nnz);
-  // those outside our rows are never read), column ids checked against K
-  // once here, marks cleared.  The loads do not wait for the row lookups
-  // above; each thread issues its loads before the first LDS store.
+  // Stage the tile's nonzeros (positions clamped to [0, nnz); those outside
+  // our rows are never read): loader source per column (checked against K
+  // once here), value bits (-0 for an invalid column), marks cleared.  The
+  // first chunk's loads are issued before the row search below, so the two
+  // overlap.
   const int64_t nr = j1 - j0;
-  if (threadIdx.x <= nr) s_cut[threadIdx.x] = -1;
+  if (threadIdx.x <= nr) {
+    s_cut[threadIdx.x] = -1;
+    s_long[threadIdx.x] = -1;
+  }
+  // rS: the row holding position P0 (tiles starting outside our positions
+  // [base, end) clamp to the row range); runs of empty rows before the tile
+  // are skipped.  Every wavefront finds it by the same search.
+  int64_t rS = g.row_hi;
   for (int64_t i0 = 0; i0 < tile_positions; i0 += kStageUnroll * blockDim.x) {
     I cs[kStageUnroll];
     T vs[kStageUnroll];
@@ -281,40 +396,49 @@ __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM
       cs[k] = col[p];
       vs[k] = value[p];
     }
+    if (i0 == 0) rS = P0 < base ? g.row_lo : (P0 < end ? find_row(g, P0) : g.row_hi);
 #pragma unroll
     for (int k = 0; k < kStageUnroll; ++k) {
       const int64_t i = i0 + k * blockDim.x + threadIdx.x;
       if (i < tile_positions) {
-        const int64_t c = static_cast<int64_t>(cs[k]);
-        const uint32_t c32 = static_cast<uint64_t>(c) < static_cast<uint64_t>(K) ? static_cast<uint32_t>(c) : kBadCol;
-        s_ent[i] = lanes::raw16_t{c32, value_bits<T>(vs[k]), 0u, 0u};
+        const uint32_t src = Loader::stage(static_cast<int64_t>(cs[k]), K, N);
+        sa.src[i] = src;
+        sa.mark[i] = 0u;
+        sa.val[i] = src != Loader::kNone ? value_bits<T>(vs[k]) : kNegZero<T>;
       }
     }
   }
   __syncthreads();
-  // Mark the starts and ends of the tile's non-empty rows (ends also in the
-  // halo); each position is marked only by the row that holds it.  A short
+  // Mark the last position of every non-empty row that ends in the tile (or
+  // its halo); each position is marked only by the row that holds it.  The
+  // tile's rows run from rS while they start at or before P1 (the row holding
+  // P1 included; later rows start in the next tile), below row_hi.  A short
   // row (at most R / SPMM_GATHER_SHORT_DIV nonzeros) that crosses a range
   // boundary is owned by the range where it starts: s_cut tells that range
-  // how far to run on and the next range where to begin.  Longer rows leave
-  // one fp32 partial per range instead.  Empty rows are left to the post pass.
-  for (int64_t r = rS + threadIdx.x; r < rE; r += blockDim.x) {
-    const int64_t a = g.rp(r), b = g.rp(r + 1);
-    if (a < b) {
-      const bool start_in = a >= P0 && a < P1 && r - rS < (INT32_MAX >> 2) - 1;
-      const bool end_in = b - 1 >= P0 && b - 1 < P0 + tile_positions;
-      if (start_in) {
-        const uint32_t vp = g.in_block_window(r) ? 2u : 0u;
-        s_word[4 * (a - P0) + 2] = static_cast<uint32_t>((r - rS + 1) << 2) | vp | (end_in && b - 1 == a ? 1u : 0u);
-      }
-      if (end_in && !(start_in && b - 1 == a)) s_word[4 * (b - 1 - P0) + 2] = 1u;
-      if (b - a <= g.range / SPMM_GATHER_SHORT_DIV) {
-        const int64_t k = a < P0 ? 0 : (a - P0) / g.range + 1;  // first boundary after a
-        if (k <= nr && P0 + k * g.range < b) s_cut[k] = static_cast<int32_t>(b - P0);
+  // how far to run on and the next range where to begin.  A longer row leaves
+  // one fp32 partial per range instead (s_long).  Empty rows are left to the
+  // post pass.
+  for (int64_t r0 = rS;; r0 += blockDim.x) {
+    const int64_t r = r0 + threadIdx.x;
+    const int64_t a = r < g.row_hi ? g.rp(r) : P1 + 1;
+    if (a <= P1) {
+      const int64_t b = g.rp(r + 1);
+      if (a < b) {
+        if (b - 1 >= P0 && b - 1 < P0 + tile_positions && r - rS < (INT32_MAX >> 1) - 1) {
+          const uint32_t vp = g.in_block_window(r) ? 1u : 0u;
+          sa.mark[b - 1 - P0] = static_cast<uint32_t>((r - rS + 1) << 1) | vp;
+        }
+        int64_t k = a < P0 ? 0 : (a - P0) / g.range + 1;  // first boundary after a
+        if (b - a <= g.range / SPMM_GATHER_SHORT_DIV) {
+          if (k <= nr && P0 + k * g.range < b) s_cut[k] = static_cast<int32_t>(b - P0);
+        } else {
+          for (; k <= nr && P0 + k * g.range < b; ++k) s_long[k] = r;
+        }
       }
     }
+    // Another chunk of rows when the chunk's last row still belongs to the tile.
+    if (!__syncthreads_or(threadIdx.x == blockDim.x - 1 && a <= P1)) break;
   }
-  __syncthreads();
 
   // Lane group -> (range j, column chunk cc).
   const int L = 1 << log2L;
@@ -339,66 +463,49 @@ __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM
   }
 
   Sink<T> sk;
-  sk.s_ent = s_ent;
   sk.rS = rS;
   sk.row_hi = g.row_hi;
   sk.out = out;
   sk.N = N;
   sk.c0 = c0;
   sk.vpart = g.vpart;
-  sk.to_vpart = false;
   sk.head_slot = ws + (2 * j) * slot + c0;
   sk.tail_slot = ws + (2 * j + 1) * slot + c0;
-  sk.rel = 0;  // set by the first row-start mark; stays 0 for a row begun earlier
+  // The first row began before the range when a long row crosses its start.
+  sk.head = cut_in < 0 && lo > base && s_long[j - j0] >= 0;
 #pragma unroll
   for (int i = 0; i < V; ++i) sk.acc[i] = 0.f;
 
-  if (K <= 0) {  // no valid column: rows still flush (as zeros)
-    Batch<T> z;
-    z.ok = 0;
-#pragma unroll
-    for (int u = 0; u < kBatch; ++u) {
-      z.v[u] = -0.0f;
-      z.x[u] = lanes::raw16_t{0, 0, 0, 0};
-    }
-    for (int32_t p0 = ps; p0 < pe; p0 += kBatch) {
-#pragma unroll
-      for (int u = 0; u < kBatch; ++u) z.m[u] = p0 + u < pe ? static_cast<int32_t>(s_ent[p0 + u].z) : 0;
-      sk.consume(z);
+  // Two batches of kBatch dense rows in flight: the loads of the next batch
+  // are issued before a batch is accumulated.  The first batch (4-aligned
+  // start, positions before ps masked) and the last two are issued masked;
+  // the steady-state loop only issues batches wholly inside [ps, pe).
+  const Stream<T, Loader> st{sa, Loader(dense, K, N, c0), ps, pe};
+  int32_t p = ps & ~(kBatch - 1);
+  Batch<T> A, B;
+  st.template issue<true>(A, p);
+  for (; p + 3 * kBatch <= pe; p += 2 * kBatch) {
+    st.template issue<false>(B, p + kBatch);
+    sk.consume(A);
+    st.template issue<false>(A, p + 2 * kBatch);
+    sk.consume(B);
+  }
+  // A holds batch p; at most two more batches start before pe.
+  if (p + kBatch < pe) {
+    st.template issue<true>(B, p + kBatch);
+    sk.consume(A);
+    if (p + 2 * kBatch < pe) {
+      st.template issue<true>(A, p + 2 * kBatch);
+      sk.consume(B);
+      sk.consume(A);
+    } else {
+      sk.consume(B);
     }
   } else {
-    // kInFlight batches of kBatch dense rows in flight: the loads of the
-    // next kInFlight-1 batches are issued before a batch is accumulated.
-    Stream<T> st;
-    st.s_ent = s_ent;
-    st.dense_c0 = dense + c0;
-    st.N = static_cast<uint32_t>(N);
-    st.pe = pe;
-    Batch<T> bq[kInFlight];
-#pragma unroll
-    for (int k = 0; k + 1 < kInFlight; ++k) st.issue(bq[k], ps + k * kBatch);
-    for (int32_t p0 = ps; p0 < pe; p0 += kInFlight * kBatch) {
-#pragma unroll
-      for (int k = 0; k < kInFlight; ++k) {
-        st.issue(bq[(k + kInFlight - 1) % kInFlight], p0 + (k + kInFlight - 1) * kBatch);
-        sk.consume(bq[k]);
-      }
-    }
+    sk.consume(A);
   }
-  const int64_t tail_row = sk.finish(pe);
+  const int64_t tail_row = sk.finish(sa.mark[pe - 1] == 0u, s_long[j - j0 + 1]);
   if (reporter) g.tail[j] = tail_row;
-}
-
-// Tile-row table: for every tile t whose first position P = t*T lies in a
-// row of [row_lo, row_hi), tile_row[t] = that row.  One thread per row writes
-// the tile starts inside its nonzero span [rp(r), rp(r+1)).
-template <typename I>
-__global__ __launch_bounds__(kWgThreads) void gather_tile_rows(Geometry<I> g, int64_t T, int64_t tiles) {
-  const int64_t r = g.row_lo + static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (r >= g.row_hi) return;
-  const int64_t a = g.rp(r), b = g.rp(r + 1);
-  const int64_t t_end = (b + T - 1) / T < tiles ? (b + T - 1) / T : tiles;
-  for (int64_t t = (a + T - 1) / T; t < t_end; ++t) g.tile_row[t] = r;
 }
 
 // Post pass, one launch:
@@ -530,24 +637,22 @@ spmm_status gather_typed(const void* rowptr, const void* col, const void* value,
   const int64_t wg_threads = groups_per_wg * L;
   const int64_t slot = gather_slot_floats(N);
 
-  // Workspace: tail rows and the tile-row table, then the partial slots
-  // (256-byte aligned).
-  const size_t tail_bytes = align_up(static_cast<size_t>(2 * g.nranges + 1) * sizeof(int64_t), 256);
+  // Workspace: tail rows, then the partial slots (256-byte aligned).
+  const size_t tail_bytes = align_up(static_cast<size_t>(g.nranges) * sizeof(int64_t), 256);
   const size_t need = tail_bytes + static_cast<size_t>(2 * g.nranges) * slot * sizeof(float);
   if (ws == nullptr || ws_bytes < need)
     return fail(SPMM_ERR_CONTRACT, "gather workspace too small: need " + std::to_string(need) +
                                        " bytes, got " + std::to_string(ws_bytes));
   g.tail = static_cast<int64_t*>(ws);
-  g.tile_row = g.tail + g.nranges;
   float* partial = reinterpret_cast<float*>(static_cast<char*>(ws) + tail_bytes);
 
   if (g.nnz > 0) {
     const int64_t tiles = ceil_div(g.nranges, ranges_per_tile);
-    hipLaunchKernelGGL((gather_tile_rows<I>), dim3(static_cast<unsigned>(ceil_div(row_hi - row_lo, kWgThreads))),
-                       dim3(kWgThreads), 0, stream, g, ranges_per_tile * g.range, tiles);
-    if (spmm_status st = check_launch("gather_tile_rows")) return st;
-    const size_t lds = static_cast<size_t>((ranges_per_tile + 1) * g.range) * sizeof(lanes::raw16_t);
-    hipLaunchKernelGGL((gather_tiles<T, I>), dim3(static_cast<unsigned>(tiles * wg_split)),
+    const size_t lds = static_cast<size_t>((ranges_per_tile + 1) * g.range) * Staged<T>::bytes_per_position();
+    // Dense operands within a 32-bit byte extent use buffer loads.
+    const bool buffer = K * N * static_cast<int64_t>(sizeof(T)) <= kBufferLimit;
+    auto kernel = buffer ? gather_tiles<T, I, BufferLoader<T>> : gather_tiles<T, I, GlobalLoader<T>>;
+    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(tiles * wg_split)),
                        dim3(static_cast<unsigned>(wg_threads)), lds, stream, g,
                        static_cast<const I*>(col), static_cast<const T*>(value),
                        static_cast<const T*>(dense), K, N, static_cast<T*>(out), partial, log2L,
@@ -567,7 +672,7 @@ spmm_status gather_typed(const void* rowptr, const void* col, const void* value,
 
 size_t gather_workspace_bytes(int64_t nnz, int64_t width) {
   const int64_t nr = (nnz > 0 ? ceil_div(nnz, gather_range(nnz)) : 1);
-  return align_up(static_cast<size_t>(2 * nr + 1) * sizeof(int64_t), 256) +
+  return align_up(static_cast<size_t>(nr) * sizeof(int64_t), 256) +
          static_cast<size_t>(2 * nr) * gather_slot_floats(width) * sizeof(float);
 }
 
