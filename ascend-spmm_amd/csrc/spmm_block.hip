@@ -75,6 +75,7 @@ struct BlockArgs {
   T* out;
   const float* vpart;      // [16*windows][N] fp32 vector sums of block-window rows (gather pass)
   float* slots;            // [noverflow][2][16][N] fp32 partials of windows longer than kbig
+  int64_t* first_of;       // [noverflow]: window whose blocks past its first chunk start in range k, or -1
   int64_t kbig, noverflow, per_xcd;
   int64_t stage;           // blocks staged in LDS at a time (multiple of the K-step)
 
@@ -275,29 +276,6 @@ __device__ inline void window_chunk(const BlockArgs<T, I>& a, int64_t s, int64_t
   }
 }
 
-// Finishes window s from an fp32 [16][N] sum in LDS (the combine kernel):
-// adds the vector sums of rows that have them, rounds once, writes the rows.
-template <typename T, typename I>
-__device__ inline void finish_window(const BlockArgs<T, I>& a, int64_t s, const float* src) {
-  constexpr int V = LaneVec<T>::V;
-  const unsigned vec = window_vector_rows(a, s);
-  const int64_t chunks = a.N / V;
-  for (int64_t it = threadIdx.x; it < 16 * chunks; it += blockDim.x) {
-    const int64_t r = it / chunks;
-    const int64_t c0 = (it - r * chunks) * V;
-    const int64_t row = 16 * s + r;
-    float acc[V];
-#pragma unroll
-    for (int i = 0; i < V; ++i) acc[i] = src[r * a.N + c0 + i];
-    if (vec >> r & 1u) {
-      const float* vp = a.vpart + row * a.N + c0;
-#pragma unroll
-      for (int i = 0; i < V; ++i) acc[i] = acc[i] + vp[i];
-    }
-    LaneVec<T>::store(a.out + row * a.N + c0, acc);
-  }
-}
-
 // Work-groups [0, 8*per_xcd): window s (XCD-aware order) computes its first
 // kbig blocks; a window with at most kbig blocks is finished here.  A longer
 // window leaves its first-chunk sum in slot (k0, 1), k0 = (b0 + kbig) / kbig.
@@ -335,38 +313,64 @@ __global__ __launch_bounds__(64 * kMaxWaves) __attribute__((amdgpu_waves_per_eu(
   int64_t first_above, unused;
   wg_lower_bound2([&](int64_t i) { return a.crp(i); }, 0, a.windows, bk + 1, bk + 1, first_above, unused);
   const int64_t s = first_above - 1;
-  if (s < 0 || s >= a.windows) return;
-  const int64_t b0 = a.crp(s), b1 = a.crp(s + 1);
-  if (!(b0 < bk && b1 > b0 + a.kbig)) return;
+  const bool valid = s >= 0 && s < a.windows;
+  const int64_t b0 = valid ? a.crp(s) : 0, b1 = valid ? a.crp(s + 1) : 0;
+  const bool owns = valid && b0 < bk && b1 > b0 + a.kbig;
+  // Range k is the first overflow range of window s exactly when block bk
+  // lies in the window's second chunk; the combine pass starts there.
+  if (threadIdx.x == 0) a.first_of[k] = owns && (b0 + a.kbig) / a.kbig == k ? s : -1;
+  if (!owns) return;
   const int64_t lo = b0 + a.kbig > bk ? b0 + a.kbig : bk;
   const int64_t hi = b1 < bk + a.kbig ? b1 : bk + a.kbig;
   if (lo >= hi) return;
   window_chunk(a, s, lo, hi, a.slots + (2 * k) * n16, s_col, s_val);
 }
 
-// Work-group k: if a window's blocks past its first chunk start in overflow
-// range k, add first chunk + segments k, k+1, ... in order (into LDS) and
-// finish the window.
+// Combine pass, one work-group per (overflow range k, slice of 4*256 fp32
+// elements of the [16][N] window tile): if a window's blocks past its first
+// chunk start in range k (first_of[k]), each thread adds first chunk +
+// segments k, k+1, ... in order for its 4 elements, then adds the row's
+// vector sum where it has one, rounds once and writes the output.
+constexpr int kCombineThreads = 256;
+constexpr int kCombineSlice = 4 * kCombineThreads;
 template <typename T, typename I>
-__global__ __launch_bounds__(256) void block_combine(BlockArgs<T, I> a) {
-  extern __shared__ float tile[];  // [16][N] fp32
-  const int64_t k = blockIdx.x;
-  const int64_t bk = k * a.kbig;
-  int64_t first_above, unused;
-  wg_lower_bound2([&](int64_t i) { return a.crp(i); }, 0, a.windows, bk + 1, bk + 1, first_above, unused);
-  const int64_t s = first_above - 1;
-  if (s < 0 || s >= a.windows) return;
-  const int64_t b0 = a.crp(s), b1 = a.crp(s + 1);
-  if (!(b1 - b0 > a.kbig && (b0 + a.kbig) / a.kbig == k)) return;
+__global__ __launch_bounds__(kCombineThreads) void block_combine(BlockArgs<T, I> a, int64_t slices) {
+  const int64_t k = static_cast<int64_t>(blockIdx.x) / slices;
+  const int64_t sl = static_cast<int64_t>(blockIdx.x) - k * slices;
+  const int64_t s = a.first_of[k];
+  if (s < 0) return;  // uniform over the work-group
+  const int64_t b1 = a.crp(s + 1);
   const int64_t k_end = (b1 - 1) / a.kbig;
   const int64_t n = 16 * a.N;
-  for (int64_t i = threadIdx.x; i < n; i += blockDim.x) {
-    float acc = a.slots[(2 * k + 1) * n + i];
-    for (int64_t kk = k; kk <= k_end; ++kk) acc = acc + a.slots[(2 * kk) * n + i];
-    tile[i] = acc;
+  const int64_t i = sl * kCombineSlice + 4 * static_cast<int64_t>(threadIdx.x);
+  if (i >= n) return;
+  const lanes::float4_t* first = reinterpret_cast<const lanes::float4_t*>(a.slots + (2 * k + 1) * n + i);
+  lanes::float4_t acc = *first;
+  constexpr int kAhead = 8;
+  for (int64_t k0 = k; k0 <= k_end; k0 += kAhead) {
+    lanes::float4_t h[kAhead];
+#pragma unroll
+    for (int u = 0; u < kAhead; ++u) {
+      const int64_t kk = k0 + u <= k_end ? k0 + u : k_end;
+      h[u] = *reinterpret_cast<const lanes::float4_t*>(a.slots + (2 * kk) * n + i);
+    }
+#pragma unroll
+    for (int u = 0; u < kAhead; ++u)
+      if (k0 + u <= k_end) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[e] = acc[e] + h[u][e];
+      }
   }
-  __syncthreads();
-  finish_window(a, s, tile);
+  const int64_t r = i / a.N, c = i - r * a.N;  // 4 elements of one row (N % 4 == 0)
+  const int64_t row = 16 * s + r;
+  if (a.row_has_vector(row)) {
+    const lanes::float4_t vp = *reinterpret_cast<const lanes::float4_t*>(a.vpart + row * a.N + c);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[e] = acc[e] + vp[e];
+  }
+  T* dst = a.out + row * a.N + c;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) dst[e] = static_cast<T>(acc[e]);
 }
 
 template <typename T, typename I>
@@ -395,6 +399,7 @@ spmm_status block_typed(const void* Crowptr, const void* Ccol, const void* Cvalu
   a.slots = slots;
   a.kbig = block_chunk_for(sizeof(T) == 2 ? SPMM_VALUE_F16 : SPMM_VALUE_F32, a.limit);
   a.noverflow = block_overflow_ranges(a.limit, a.kbig);
+  a.first_of = reinterpret_cast<int64_t*>(slots + a.noverflow * 2 * 16 * N);
   a.per_xcd = ceil_div(windows, kXcds);
   const int64_t groups = (N + 63) / 64;
   const int waves = groups < kMaxWaves ? static_cast<int>(groups) : kMaxWaves;
@@ -411,9 +416,9 @@ spmm_status block_typed(const void* Crowptr, const void* Ccol, const void* Cvalu
                      stage_lds, stream, a);
   if (spmm_status st = check_launch("block_windows")) return st;
   if (a.noverflow == 0) return SPMM_OK;
-  const size_t tile_lds = static_cast<size_t>(16) * N * sizeof(float);
-  hipLaunchKernelGGL((block_combine<T, I>), dim3(static_cast<unsigned>(a.noverflow)), dim3(256), tile_lds,
-                     stream, a);
+  const int64_t slices = ceil_div(16 * N, kCombineSlice);
+  hipLaunchKernelGGL((block_combine<T, I>), dim3(static_cast<unsigned>(a.noverflow * slices)),
+                     dim3(kCombineThreads), 0, stream, a, slices);
   return check_launch("block_combine");
 }
 

@@ -112,7 +112,8 @@ int64_t spmm_mixed_out_rows(const spmm_mixed_desc* d) {
 namespace {
 // Workspace of the mixed operator: gather part, then the fp32 vector sums of
 // block-window rows ([16*windows][width]), then the pieces of windows longer
-// than the block chunk ([ranges][2][16][width]).
+// than the block chunk ([ranges][2][16][width]) and the window starting in
+// each overflow range ([ranges] int64).
 struct MixedLayout {
   size_t gather = 0, vpart = 0, slots = 0;
   int64_t limit = 0;
@@ -126,7 +127,8 @@ struct MixedLayout {
     limit = d->block_count < d->block_values / 16 ? d->block_count : d->block_values / 16;
     if (limit < 0) limit = 0;
     const int64_t ranges = block_overflow_ranges(limit, block_chunk_for(d->value_type, limit));
-    slots = align_up(static_cast<size_t>(ranges * 2 * 16) * w * sizeof(float), 256);
+    slots = align_up(static_cast<size_t>(ranges * 2 * 16) * w * sizeof(float) +
+                         static_cast<size_t>(ranges) * sizeof(int64_t), 256);
   }
   size_t total() const { return gather + vpart + slots; }
 };
