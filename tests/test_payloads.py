@@ -1,4 +1,4 @@
-"""The harness's dataset format (ascend-spmm_amd/datasets.py): payload
+"""The harness's dataset format (ascend-spmm_amd/payloads.py): payload
 round trips, each validation error of the reference's load_payload
 (tests/task_mapping/common.py:33-63), discovery and selection, stable_seed,
 and Matrix Market conversion (tests/data/prepare_data.py:25-42)."""
@@ -14,7 +14,7 @@ import torch
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 sys.path.insert(0, os.path.join(REPO, "ascend-spmm_amd"))
 
-import datasets as D  # noqa: E402
+import payloads as D  # noqa: E402
 
 
 def write(path, **payload):
