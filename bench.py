@@ -55,9 +55,9 @@ MFMA_PEAK_TFLOPS = {"fp16": 2500.0, "fp32": 157.3}
 FETCH_SCALE = 2.0
 WRITE_SCALE = 1.0
 PMC_KIB = {
-    (2, "csr", 128): {"fetch_kib": 210194.4 + 3876.9 + 245.7, "write_kib": 31379.3 + 659.8 + 16.4},
-    (3, "mixed", 128): {"fetch_kib": 122641.8 + 6310.1 + 169.6 + 131694.9 + 103.5,
-                        "write_kib": 12090.3 + 2266.5 + 8.1 + 14116.0 + 0.0},
+    (2, "csr", 128): {"fetch_kib": 211921.8 + 3878.9, "write_kib": 31383.2 + 659.8},
+    (3, "mixed", 128): {"fetch_kib": 129109.9 + 6312.1 + 131730.0 + 160.0,
+                        "write_kib": 12093.7 + 2266.5 + 14184.6 + 0.0},
 }
 
 def log(msg: str) -> None:
