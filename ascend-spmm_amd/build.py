@@ -31,6 +31,7 @@ HIP_SOURCES = [
     "spmm_block.hip",
     "permute_rows.hip",
     "spmm_cubeop.hip",
+    "spmm_rowscalar.hip",
     "preprocess.hip",
 ]
 

@@ -69,6 +69,11 @@ spmm_status launch_gather(int32_t index_type, int32_t value_type,
                           const void* Crowptr, int64_t cwin, int64_t climit, float* vpart,
                           hipStream_t stream);
 
+// Thread-per-row scalar CSR baseline over rows [0, rows) (no workspace).
+spmm_status launch_rowscalar(int32_t index_type, int32_t value_type, const void* rowptr, const void* col,
+                             const void* value, int64_t rows, int64_t nnz, const void* dense, int64_t K,
+                             int64_t N, void* out, hipStream_t stream);
+
 // Workspace bytes launch_gather may use for at most `nnz` vector nonzeros.
 size_t gather_workspace_bytes(int64_t nnz, int64_t width);
 

@@ -102,6 +102,25 @@ spmm_status spmm_csr_run(const spmm_csr_desc* d, const void* rowptr, const void*
                        nullptr, as_stream(stream));
 }
 
+spmm_status spmm_csr_rowscalar_run(const spmm_csr_desc* d, const void* rowptr, const void* col,
+                                   const void* value, const void* dense, void* out, spmm_stream stream) {
+  clear_error();
+  if (d == nullptr) return fail(SPMM_ERR_INVALID_ARGUMENT, "null descriptor");
+  if (spmm_status st = check_types(d->index_type, d->value_type, "spmm_csr_rowscalar")) return st;
+  if (spmm_status st = check_width(d->width, d->value_type, d->value_type == SPMM_VALUE_F16 ? 16 : 8,
+                                   "spmm_csr_rowscalar"))
+    return st;
+  if (d->rows < 0 || d->nnz < 0 || d->dense_rows < 0)
+    return fail(SPMM_ERR_CONTRACT, "spmm_csr_rowscalar: negative extent");
+  if (d->rows == 0) return SPMM_OK;
+  if (rowptr == nullptr || out == nullptr || (d->nnz > 0 && (col == nullptr || value == nullptr)) ||
+      (d->dense_rows > 0 && dense == nullptr))
+    return fail(SPMM_ERR_INVALID_ARGUMENT, "spmm_csr_rowscalar: null device pointer");
+  if (spmm_status st = check_aligned(dense, out, "spmm_csr_rowscalar")) return st;
+  return launch_rowscalar(d->index_type, d->value_type, rowptr, col, value, d->rows, d->nnz, dense,
+                          d->dense_rows, d->width, out, as_stream(stream));
+}
+
 int64_t spmm_mixed_out_rows(const spmm_mixed_desc* d) {
   if (d == nullptr) return -1;
   const int64_t blocks = 16 * (d->block_windows < 0 ? 0 : d->block_windows);

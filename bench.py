@@ -26,6 +26,7 @@ Only one GPU is used; --gpus > 1 exits with a message.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -163,6 +164,30 @@ def mixed_operands(spmm_npu, w, dev, graph_layout: bool):
     return ops, cstart, vstart, p
 
 
+class _CsrDesc(ctypes.Structure):
+    _fields_ = [("rows", ctypes.c_int64), ("nnz", ctypes.c_int64), ("dense_rows", ctypes.c_int64),
+                ("width", ctypes.c_int64), ("index_type", ctypes.c_int32), ("value_type", ctypes.c_int32)]
+
+
+def rowscalar_ms(crow, col, val, dense, w) -> float:
+    """HIP-event ms per call of the thread-per-row scalar CSR baseline
+    (spmm_csr_rowscalar_run of the C ABI; one thread per output row), 1
+    warm-up and 3 timed calls."""
+    lib = ctypes.CDLL(os.path.join(REPO, "ascend-spmm_amd", "libspmm_mi355x.so"))
+    lib.spmm_last_error.restype = ctypes.c_char_p
+    out = torch.empty(w.rows, dense.shape[1], dtype=dense.dtype, device=dense.device)
+    d = _CsrDesc(w.rows, w.nnz, w.cols, dense.shape[1], 0, 0 if dense.dtype == torch.float16 else 1)
+    p = lambda t: ctypes.c_void_p(t.data_ptr())
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def step():
+        rc = lib.spmm_csr_rowscalar_run(ctypes.byref(d), p(crow), p(col), p(val), p(dense), p(out), stream)
+        if rc != 0:
+            raise RuntimeError(lib.spmm_last_error().decode())
+
+    return time_calls(step, 3, 1)[1]
+
+
 def block_path(spmm_npu, dev, steps: int, warmup: int) -> dict:
     """Config 3 (block-banded) at N=128 fp16: spmm_ascend_cube on the output
     of the GPU preprocess (the reference's headline pipeline) and on the
@@ -181,6 +206,7 @@ def block_path(spmm_npu, dev, steps: int, warmup: int) -> dict:
             torch.zeros(0, dtype=val.dtype, device=dev))
     bstart = spmm_npu.make_start(b["crow_window_ptr"], 20).to(dev)
     _, csr_ms = time_calls(lambda: spmm_npu.spmm_csr(crow, col, val, dense, start), steps, warmup)
+    scalar_ms = rowscalar_ms(crow, col, val, dense, w)
     _, mixed_ms = time_calls(lambda: spmm_npu.spmm_ascend_cube(*ops, dense, cstart, vstart), steps, warmup)
     _, bcsr_ms = time_calls(lambda: spmm_npu.spmm_ascend_cube(*bops, dense, bstart, start), steps, warmup)
     nblk = int(p["crow_window_ptr"][-1].item())
@@ -198,6 +224,9 @@ def block_path(spmm_npu, dev, steps: int, warmup: int) -> dict:
         "preprocess_aic_blocks_16x1": nblk,
         "preprocess_vector_nnz": int(p["vvalue"].numel()),
         "bcsr_blocks_16x1": nblk_all,
+        "rowscalar_csr_ms": round(scalar_ms, 5),
+        "speedup_preprocess_vs_rowscalar": round(scalar_ms / mixed_ms, 2),
+        "speedup_bcsr_vs_rowscalar": round(scalar_ms / bcsr_ms, 2),
         "bcsr_mfma_executed_tflops": round(mfma_tflops, 2),
         "bcsr_mfma_utilisation": round(mfma_tflops / MFMA_PEAK_TFLOPS["fp16"], 4),
     }

@@ -93,6 +93,15 @@ spmm_status spmm_csr_run(const spmm_csr_desc* desc,
                          void* workspace, size_t workspace_bytes,
                          spmm_stream stream);
 
+/* Thread-per-row scalar CSR SpMM, same arguments and result contract as
+ * spmm_csr_run (same sums in the same order within a row; no workspace).
+ * No counterpart in the reference: it is the baseline that the block path's
+ * speed-up is stated against (one thread per output row, nonzeros in order,
+ * 16-byte pieces of the dense row), for callers comparing kernels. */
+spmm_status spmm_csr_rowscalar_run(const spmm_csr_desc* desc,
+                                   const void* rowptr, const void* col, const void* value,
+                                   const void* dense, void* out, spmm_stream stream);
+
 /* ------------------------------------------------------------------------
  * spmm_mixed — the spmm_ascend_cube operator:
  *   out[16*s + r, :]  = sum_{b in [Crowptr[s], Crowptr[s+1])} Cvalue[16*b + r] * dense[Ccol[b], :]

@@ -125,3 +125,53 @@ def test_direct_cabi_calls_match_oracle(lib):
     assert rc == 0, lib.spmm_last_error()
     torch.cuda.synchronize()
     assert torch.equal(out.cpu(), out2.cpu())
+
+
+def test_rowscalar_host_validation(lib):
+    d = CsrDesc(10, 5, 10, 24, 0, 0)
+    assert lib.spmm_csr_rowscalar_run(ctypes.byref(d), None, None, None, None, None, None) == 4
+    assert b"spmm_csr_rowscalar requires feature width divisible by 16" in lib.spmm_last_error()
+    d = CsrDesc(10, 5, 10, 16, 0, 0)
+    assert lib.spmm_csr_rowscalar_run(ctypes.byref(d), None, None, None, None, None, None) == 1
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("value_type,N", [(0, 16), (0, 128), (1, 8), (1, 64)])
+def test_rowscalar_baseline_matches_oracle_and_csr(lib, value_type, N):
+    """The thread-per-row baseline computes the same row sums as spmm_csr:
+    within tolerance of fp64 everywhere, bitwise on rows that spmm_csr sums
+    in one piece (at most R/2 nonzeros; R = 16 for this size)."""
+    import torch
+
+    import oracle as O
+
+    rng = np.random.default_rng(9 + N)
+    rows, K = 300, 180
+    deg = rng.integers(0, 25, rows)
+    crow = np.zeros(rows + 1, np.int64)
+    crow[1:] = np.cumsum(deg)
+    col = np.concatenate([np.sort(rng.choice(K, d, replace=False)) for d in deg]).astype(np.int64)
+    col[::17] = K + 3  # invalid columns contribute zero
+    npdt = np.float16 if value_type == 0 else np.float32
+    vals = rng.uniform(-1, 1, col.size).astype(npdt)
+    B = rng.standard_normal((K, N)).astype(npdt)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    d_crow, d_col, d_val, d_B = t(crow.astype(np.int32)), t(col.astype(np.int32)), t(vals), t(B)
+    out = torch.empty(rows, N, dtype=d_B.dtype, device="cuda")
+    ref = torch.empty_like(out)
+    d = CsrDesc(rows, col.size, K, N, 0, value_type)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    p = lambda x: ctypes.c_void_p(x.data_ptr())
+    assert lib.spmm_csr_rowscalar_run(ctypes.byref(d), p(d_crow), p(d_col), p(d_val), p(d_B), p(out), stream) == 0
+    ws_bytes = ctypes.c_size_t(0)
+    assert lib.spmm_csr_workspace(ctypes.byref(d), ctypes.byref(ws_bytes)) == 0
+    ws = torch.empty(max(ws_bytes.value, 1), dtype=torch.uint8, device="cuda")
+    assert lib.spmm_csr_run(ctypes.byref(d), p(d_crow), p(d_col), p(d_val), p(d_B), p(ref), p(ws),
+                            ctypes.c_size_t(ws_bytes.value), stream) == 0, lib.spmm_last_error()
+    torch.cuda.synchronize()
+    tol = 2e-2 if value_type == 0 else 1e-4
+    keep = col < K
+    expected = O.spmm_f64(crow, np.where(keep, col, 0), np.where(keep, vals, 0).astype(npdt), B)
+    assert np.allclose(out.float().cpu().numpy(), expected, atol=tol, rtol=tol)
+    short = deg <= 8
+    assert torch.equal(out.cpu()[torch.from_numpy(short)], ref.cpu()[torch.from_numpy(short)])
