@@ -29,6 +29,10 @@ inline hipStream_t as_stream(spmm_stream s) { return reinterpret_cast<hipStream_
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// XCDs of an MI355X.  Work-groups are dispatched round-robin over them, so
+// work-group g runs on XCD g % kXcds and shares that XCD's L2 with g +- kXcds.
+constexpr int kXcds = 8;
+
 inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
 // Split length R of the CSR gather path: nonzero positions are cut into

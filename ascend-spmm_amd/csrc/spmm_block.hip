@@ -52,7 +52,6 @@ typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kXcds = 8;
 // Waves per window work-group: one per 64-column group, up to this many (the
 // rest loop), so wide outputs do not lengthen each wave's chain of K-steps.
 #ifndef SPMM_BLOCK_MAX_WAVES

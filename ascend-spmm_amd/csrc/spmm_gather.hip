@@ -72,6 +72,11 @@ constexpr int kStageUnroll = 8;             // staging loads issued per thread b
 #endif
 // Ranges per work-group tile (the tile stages ranges * R nonzeros in LDS).
 constexpr int64_t kTileRanges = SPMM_GATHER_TILE_RANGES;
+// Consecutive tiles one XCD (group) takes before the next group's run.
+#ifndef SPMM_GATHER_XCD_RUN
+#define SPMM_GATHER_XCD_RUN 16
+#endif
+constexpr int64_t kXcdRun = SPMM_GATHER_XCD_RUN;
 
 template <typename I>
 struct Geometry {
@@ -349,7 +354,8 @@ template <typename T, typename I, typename Loader>
 __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM_GATHER_WAVES))) void gather_tiles(
     Geometry<I> g, const I* __restrict__ col, const T* __restrict__ value,
     const T* __restrict__ dense, int64_t K, int64_t N, T* __restrict__ out, float* __restrict__ ws,
-    int log2L, int64_t chunks, int64_t ranges_per_tile, int64_t slot, int wg_split) {
+    int log2L, int64_t chunks, int64_t ranges_per_tile, int64_t slot, int wg_split, int64_t tiles,
+    int64_t tiles_per_group) {
   constexpr int V = LaneVec<T>::V;
   extern __shared__ __align__(16) unsigned char smem[];
   // The tile's positions plus a halo of one range: a short row that starts
@@ -362,11 +368,15 @@ __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM
   __shared__ int32_t s_cut[kTileRanges + 1];
   __shared__ int64_t s_long[kTileRanges + 1];
 
-  // wg_split > 1: the tile's column chunks go to wg_split work-groups (chunk
-  // = blockIdx % wg_split); consecutive blockIdx land on different XCDs, so
-  // each XCD's L2 serves one chunk of the dense rows.
-  const int64_t tile = static_cast<int64_t>(blockIdx.x) / wg_split;
-  const int64_t part = static_cast<int64_t>(blockIdx.x) % wg_split;
+  // XCD-aware tile order: the XCD of work-group g (g % kXcds) takes column
+  // part g % kXcds % wg_split of a contiguous run of tiles, so neighbouring
+  // tiles, whose rows tend to share dense rows, share an L2, and with
+  // wg_split > 1 each XCD's L2 serves one column chunk of the dense rows.
+  const int64_t xcd = static_cast<int64_t>(blockIdx.x) % kXcds;
+  const int64_t part = xcd % wg_split;
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) / kXcds;
+  const int64_t tile = ((idx / kXcdRun) * (kXcds / wg_split) + xcd / wg_split) * kXcdRun + idx % kXcdRun;
+  if (tile >= tiles) return;  // uniform over the work-group, before any barrier
   const int64_t j0 = tile * ranges_per_tile;
   const int64_t j1 = (j0 + ranges_per_tile < g.nranges) ? j0 + ranges_per_tile : g.nranges;
   const int64_t P0 = g.lo(j0), P1 = g.hi(j1 - 1);
@@ -628,7 +638,7 @@ spmm_status gather_typed(const void* rowptr, const void* col, const void* value,
       L >>= 1;
       chunks = 2;
     }
-    wg_split = static_cast<int>(chunks);
+    wg_split = static_cast<int>(chunks);  // 2: lanes_needed <= 128 and L = 64 for the widest rows
   }
   int64_t ranges_per_tile = (kWgThreads / L) / (chunks / wg_split);
   if (ranges_per_tile > kTileRanges) ranges_per_tile = kTileRanges;
@@ -652,11 +662,15 @@ spmm_status gather_typed(const void* rowptr, const void* col, const void* value,
     // Dense operands within a 32-bit byte extent use buffer loads.
     const bool buffer = K * N * static_cast<int64_t>(sizeof(T)) <= kBufferLimit;
     auto kernel = buffer ? gather_tiles<T, I, BufferLoader<T>> : gather_tiles<T, I, GlobalLoader<T>>;
-    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(tiles * wg_split)),
+    // kXcds / wg_split groups of XCDs take runs of kXcdRun tiles in turn.
+    if (kXcds % wg_split != 0) return fail(SPMM_ERR_CONTRACT, "gather: column split does not divide the XCDs");
+    const int64_t groups = kXcds / wg_split;
+    const int64_t tiles_per_group = ceil_div(tiles, groups * kXcdRun) * kXcdRun;
+    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(kXcds * tiles_per_group)),
                        dim3(static_cast<unsigned>(wg_threads)), lds, stream, g,
                        static_cast<const I*>(col), static_cast<const T*>(value),
                        static_cast<const T*>(dense), K, N, static_cast<T*>(out), partial, log2L,
-                       chunks, ranges_per_tile, slot, wg_split);
+                       chunks, ranges_per_tile, slot, wg_split, tiles, tiles_per_group);
     if (spmm_status st = check_launch("gather_tiles")) return st;
   }
   const int64_t fix_items = g.nnz > 0 ? (g.nranges - 1) * chunks * L : 0;
