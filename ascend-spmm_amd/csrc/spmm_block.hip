@@ -52,6 +52,13 @@ typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 
+// XCD-aware window order: XCDs take runs of this many consecutive windows in
+// turn, so neighbouring windows share an L2 while windows of every density
+// (the preprocess layout sorts them by density) spread over all XCDs.
+#ifndef SPMM_BLOCK_XCD_RUN
+#define SPMM_BLOCK_XCD_RUN 16
+#endif
+constexpr int64_t kBlockXcdRun = SPMM_BLOCK_XCD_RUN;
 // Waves per window work-group: one per 64-column group, up to this many (the
 // rest loop), so wide outputs do not lengthen each wave's chain of K-steps.
 #ifndef SPMM_BLOCK_MAX_WAVES
@@ -275,7 +282,7 @@ __device__ inline void window_chunk(const BlockArgs<T, I>& a, int64_t s, int64_t
   }
 }
 
-// Work-groups [0, 8*per_xcd): window s (XCD-aware order) computes its first
+// Work-groups [0, 8*per_xcd): window s (XCD-aware runs) computes its first
 // kbig blocks; a window with at most kbig blocks is finished here.  A longer
 // window leaves its first-chunk sum in slot (k0, 1), k0 = (b0 + kbig) / kbig.
 // Work-groups 8*per_xcd + k: overflow range k = blocks [k*kbig, (k+1)*kbig).
@@ -294,7 +301,8 @@ __global__ __launch_bounds__(64 * kMaxWaves) __attribute__((amdgpu_waves_per_eu(
   const int64_t g = blockIdx.x;
   const int64_t n16 = 16 * a.N;
   if (g < lead) {
-    const int64_t s = (g % kXcds) * a.per_xcd + g / kXcds;
+    const int64_t idx = g / kXcds;
+    const int64_t s = ((idx / kBlockXcdRun) * kXcds + g % kXcds) * kBlockXcdRun + idx % kBlockXcdRun;
     if (s >= a.windows) return;  // uniform over the work-group
     const int64_t b0 = a.crp(s);
     int64_t b1 = a.crp(s + 1);
@@ -399,7 +407,7 @@ spmm_status block_typed(const void* Crowptr, const void* Ccol, const void* Cvalu
   a.kbig = block_chunk_for(sizeof(T) == 2 ? SPMM_VALUE_F16 : SPMM_VALUE_F32, a.limit);
   a.noverflow = block_overflow_ranges(a.limit, a.kbig);
   a.first_of = reinterpret_cast<int64_t*>(slots + a.noverflow * 2 * 16 * N);
-  a.per_xcd = ceil_div(windows, kXcds);
+  a.per_xcd = ceil_div(windows, kXcds * kBlockXcdRun) * kBlockXcdRun;
   const int64_t groups = (N + 63) / 64;
   const int waves = groups < kMaxWaves ? static_cast<int>(groups) : kMaxWaves;
   // Staging piece: about twice the mean window, 64 blocks up to a 20 KB LDS
