@@ -362,3 +362,74 @@ def test_spmm_cube_contract_errors(spmm_npu):
         spmm_npu.spmm_cube(rp, c, dev(np.ones(1, np.float32)), dev(np.ones((2, 8), np.float32)), zero_start(20))
     with pytest.raises(RuntimeError, match="col and value must be same size"):
         spmm_npu.spmm_cube(rp, c, dev(np.ones(2, np.float16)), dev(np.ones((2, 16), np.float16)), zero_start(20))
+
+
+def test_spmm_csr_sparse_rows_with_long_empty_gaps(spmm_npu):
+    """Few nonzeros over many rows: a tile's rows run far past 256 (the
+    marking walk takes several chunks), leading and trailing empty rows, and
+    long runs of empty rows between nonzero rows are written as zeros."""
+    rng = np.random.default_rng(71)
+    rows, K = 200000, 5000
+    nonempty = np.sort(rng.choice(np.arange(1000, rows - 1000), 2500, replace=False))
+    deg = np.zeros(rows, np.int64)
+    deg[nonempty] = rng.integers(1, 4, nonempty.size)
+    deg[nonempty[::97]] = 40  # a few rows longer than half a range
+    crow = np.zeros(rows + 1, np.int64)
+    crow[1:] = np.cumsum(deg)
+    col = np.concatenate([np.sort(rng.choice(K, d, replace=False)) for d in deg if d]).astype(np.int64)
+    for dtype in ("fp16", "fp32"):
+        vals = rng.uniform(-1, 1, col.size).astype(NP_DT[dtype])
+        B = rng.standard_normal((K, 32)).astype(NP_DT[dtype])
+        out = run_csr(spmm_npu, crow, col, vals, B)
+        assert_close(out, O.spmm_f64(crow, col, vals, B), dtype)
+        assert bool((out[torch.from_numpy(deg == 0).cuda()] == 0).all())
+
+
+def test_invalid_columns_and_nonfinite_values_stay_in_their_rows(spmm_npu):
+    """Negative and >= K column ids contribute nothing, even with an Inf
+    value; Inf values of valid columns reach only their own rows (the masked
+    edge positions of a range never leak into a neighbouring row)."""
+    rng = np.random.default_rng(72)
+    crow, col = random_csr(rng, 3000, 400, 12, long_rows=[(10, 300), (2000, 390)])
+    vals = rng.uniform(-1, 1, col.size).astype(np.float32)
+    bad = rng.choice(col.size, 60, replace=False)
+    col[bad[:30]] = -5
+    col[bad[30:]] = 400 + 7
+    vals[bad] = np.inf  # invalid columns: ignored even though their value is Inf
+    hot = rng.choice(np.setdiff1d(np.arange(col.size), bad), 25, replace=False)
+    vals[hot] = np.inf
+    B = (rng.standard_normal((400, 64)) + 8.0).astype(np.float32)  # no zeros: Inf * x stays +-Inf
+    keep = (col >= 0) & (col < 400)
+    expected = O.spmm_f64(crow, np.where(keep, col, 0), np.where(keep, vals, 0.0), B)
+    for index_dtype in (torch.int32, torch.int64):
+        out = run_csr(spmm_npu, crow, col, vals, B, index_dtype).cpu().double()
+        e = torch.from_numpy(expected)
+        finite = torch.isfinite(e)
+        assert torch.equal(torch.isfinite(out), finite)
+        assert torch.equal(torch.isnan(out), torch.isnan(e))
+        assert bool(torch.isclose(out[finite], e[finite], atol=1e-4, rtol=1e-4).all())
+
+
+def test_dense_operand_beyond_32bit_extent(spmm_npu):
+    """A dense operand larger than 4 GB (fp32, K = 2.2M rows of N = 512)
+    takes the 64-bit global-load path; columns in the last rows are read."""
+    K, N, rows = 2_200_000, 512, 600
+    rng = np.random.default_rng(73)
+    B = torch.empty((K, N), dtype=torch.float32, device="cuda")
+    B.normal_(generator=torch.Generator(device="cuda").manual_seed(5))
+    assert K * N * 4 > 0xFFFFF000
+    deg = rng.integers(0, 20, rows)
+    crow = np.zeros(rows + 1, np.int64)
+    crow[1:] = np.cumsum(deg)
+    col = np.concatenate([np.sort(rng.choice(K, d, replace=False)) for d in deg]).astype(np.int64)
+    col[:50] = np.sort(rng.choice(np.arange(K - 1000, K), 50, replace=False))  # the far end of B
+    col[60] = K + 1  # invalid
+    vals = rng.uniform(-1, 1, col.size).astype(np.float32)
+    out = spmm_npu.spmm_csr(dev(crow, torch.int32), dev(col, torch.int32), dev(vals), B,
+                            dev(O.make_start(crow, 40)))
+    used = np.unique(col[col < K])
+    Bsub = B[torch.from_numpy(used).cuda()].cpu().numpy()
+    remap = np.where(col < K, np.searchsorted(used, np.minimum(col, K - 1)), used.size + 5)
+    assert_close(out, O.spmm_f64(crow, remap, vals, Bsub), "fp32")
+    del B
+    torch.cuda.empty_cache()
