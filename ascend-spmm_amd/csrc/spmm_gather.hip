@@ -58,7 +58,10 @@ constexpr int kWgThreads = 256;
 #define SPMM_GATHER_BATCH 4
 #endif
 constexpr int kBatch = SPMM_GATHER_BATCH;  // dense rows per batch
-constexpr int kStageUnroll = 8;             // staging loads issued per thread before storing
+// Staging positions per thread and round: one round covers a tile of up to
+// 18 * 256 positions (16 + 1 ranges of R <= 256), so its loads are all in
+// flight together.
+constexpr int kStageUnroll = 18;
 // A row is "short" (summed by one lane group, never split) when it holds at
 // most R / SPMM_GATHER_SHORT_DIV nonzeros.
 #ifndef SPMM_GATHER_SPLIT_BYTES
@@ -401,10 +404,12 @@ __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM
     T vs[kStageUnroll];
 #pragma unroll
     for (int k = 0; k < kStageUnroll; ++k) {
-      int64_t p = P0 + i0 + k * blockDim.x + threadIdx.x;
-      p = p < g.nnz ? p : g.nnz - 1;
-      cs[k] = col[p];
-      vs[k] = value[p];
+      if (i0 + k * blockDim.x < tile_positions) {  // uniform over the work-group
+        int64_t p = P0 + i0 + k * blockDim.x + threadIdx.x;
+        p = p < g.nnz ? p : g.nnz - 1;
+        cs[k] = col[p];
+        vs[k] = value[p];
+      }
     }
     if (i0 == 0) rS = P0 < base ? g.row_lo : (P0 < end ? find_row(g, P0) : g.row_hi);
 #pragma unroll
