@@ -1,6 +1,6 @@
 """Benchmark of the MI355X SpMM hot path (one JSON line on stdout).
 
-Default workload: BASELINE config 2 (power-law CSR 100000x100000, ~1.9M nnz,
+Default workload: benchmark configuration 2 (power-law CSR 100000x100000, ~1.9M nnz,
 N=128 fp16, fp32 accumulate) — the configuration the headline metric
 "SpMM GFLOP/s (2*nnz*N/t) and HBM GB/s % of peak, N=128 fp16" is quoted on.
 A step is one SpMM call over resident device inputs.
@@ -354,7 +354,7 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp16" if w.dtype == "fp16" else "fp32",
-        "data": "synthetic (seeded generator of BASELINE config %d)" % args.config,
+        "data": "synthetic (seeded generator of benchmark configuration %d)" % args.config,
         "config": {
             "workload": f"{w.name} {w.rows}x{w.cols} nnz={w.nnz} N={width} {w.dtype}",
             "op": op_name,

@@ -172,7 +172,7 @@ def test_preprocess_hand_example(spmm_npu):
 
 
 def test_preprocess_config4_full_size(spmm_npu):
-    """BASELINE config 4 (200000 rows, ~3.6M nnz) at full size, bit-exact."""
+    """Benchmark configuration 4 (200000 rows, ~3.6M nnz) at full size, bit-exact."""
     w = W.config4()
     c32, k32 = w.crow.astype(np.int32), w.col.astype(np.int32)
     ref = O.preprocess(c32, k32, w.values, w.rows, w.cols, 16, False)

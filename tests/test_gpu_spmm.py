@@ -293,7 +293,7 @@ def test_pack_restore_match_oracle(spmm_npu):
 
 
 def test_config2_full_size_matches_oracle(spmm_npu):
-    """BASELINE config 2 at full size (power-law, fp16, N=128) vs the fp64 oracle."""
+    """Benchmark configuration 2 at full size (power-law, fp16, N=128) vs the fp64 oracle."""
     w = W.config2()
     B = w.dense(128)
     out = run_csr(spmm_npu, w.crow, w.col, w.values, B)

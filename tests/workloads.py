@@ -1,4 +1,4 @@
-"""Seeded synthetic CSR workloads for the five BASELINE.json configurations.
+"""Seeded synthetic CSR workloads for the five benchmark configurations (1-5).
 
 All generators use ``numpy.random.Generator(PCG64(2027 + config_id))`` (2027 is
 the reference's default base seed, tests/task_mapping/correctness.py:92) and
