@@ -83,12 +83,14 @@ size_t gather_workspace_bytes(int64_t nnz, int64_t width);
 
 // Blocks of a window handled by one work-group before the window is split
 // into chunks that separate work-groups sum and a combine pass adds in
-// order.  It grows with the total block count (at most about 16384 chunks,
-// 4096 blocks per chunk at most), so large inputs keep the partial sums (and
-// their workspace) small; it depends on the value type and the block count
-// only, never on the width, so results do not depend on the width.
+// order.  Large enough that ordinary windows are never split (each overflow
+// range costs a work-group and a window search), and growing with the total
+// block count (at most about 16384 chunks, 4096 blocks per chunk at most),
+// so large inputs keep the partial sums (and their workspace) small; it
+// depends on the value type and the block count only, never on the width,
+// so results do not depend on the width.
 inline int64_t block_chunk_for(int32_t value_type, int64_t blocks) {
-  int64_t k = value_type == SPMM_VALUE_F16 ? 512 : 256;
+  int64_t k = value_type == SPMM_VALUE_F16 ? 2048 : 1024;
   while (k < 4096 && blocks / k > 16384) k *= 2;
   return k;
 }

@@ -433,3 +433,39 @@ def test_dense_operand_beyond_32bit_extent(spmm_npu):
     assert_close(out, O.spmm_f64(crow, remap, vals, Bsub), "fp32")
     del B
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("dtype,width", [("fp16", 64), ("fp16", 512), ("fp32", 64), ("fp32", 512)])
+def test_windows_longer_than_the_block_chunk(spmm_npu, dtype, width):
+    """Windows of thousands of 16x1 blocks are cut into chunks summed by
+    separate work-groups (overflow ranges) and added in order by the combine
+    pass, which also adds the vector part of rows that have one."""
+    rng = np.random.default_rng(91 + width)
+    rows, K = 80, 20000
+    deg = np.full(rows, 3)
+    deg[16:32] = 1000          # window 1: ~11k distinct columns -> several chunks
+    deg[48:56] = 2500          # window 3: half its rows long
+    parts = [np.sort(rng.choice(K, d, replace=False)) for d in deg]
+    crow = np.zeros(rows + 1, np.int64)
+    crow[1:] = np.cumsum(deg)
+    col = np.concatenate(parts).astype(np.int64)
+    vals = rng.uniform(-1, 1, col.size).astype(NP_DT[dtype])
+    B = rng.standard_normal((K, width)).astype(NP_DT[dtype])
+    expected = O.spmm_f64(crow, col, vals, B)
+    i32 = torch.int32
+    b = O.csr_to_bcsr(crow, col, vals, rows, K, 16)
+    nblk = np.diff(b["crow_window_ptr"])
+    assert nblk.max() > 4096  # longer than any chunk for this block count
+    out = spmm_npu.spmm_ascend_cube(dev(b["crow_window_ptr"], i32), dev(b["unique_col_ids"], i32),
+                                    dev(b["value"]), zero_start(1), torch.zeros(0, dtype=i32, device="cuda"),
+                                    torch.zeros(0, dtype=dev(vals).dtype, device="cuda"), dev(B),
+                                    dev(O.make_start(b["crow_window_ptr"], 20)), zero_start(40))
+    assert_close(out[:rows], expected, dtype)
+    # the same windows with part of every row in the vector part (vpart handed to the combine)
+    h = O.block_level_split(crow, col, vals, rows, K, 1.0, 16)
+    assert h["vcol_indices"].size > 0 and np.diff(h["crow_window_ptr"]).max() > 4096
+    out = spmm_npu.spmm_ascend_cube(
+        dev(h["crow_window_ptr"], i32), dev(h["unique_col_ids"], i32), dev(h["value"]),
+        dev(h["vrow_window_ptr"], i32), dev(h["vcol_indices"], i32), dev(h["vvalue"]), dev(B),
+        dev(O.make_start(h["crow_window_ptr"], 20)), dev(O.make_start(h["vrow_window_ptr"], 40)))
+    assert_close(out[:rows], expected, dtype)
