@@ -15,26 +15,28 @@
 //    only on the positions and nnz, so every output element sees the same
 //    fp32 operation sequence for every width N: results are deterministic and
 //    bit-identical across widths.
-//  * gather_tile_rows (one thread per row) records, for every tile, the row
-//    holding the tile's first position.
-//  * gather_tiles: a work-group takes a tile of consecutive ranges.  It reads
-//    its row span from that table while it stages the tile's column ids and
-//    values in LDS (one round trip), then marks, per position, the row that
-//    starts there.  Each lane group then
-//    streams its range flat: the dense rows of 4 consecutive nonzeros are
-//    loaded together, two batches in flight (16 bytes per lane; the L lanes
-//    of a group read L*16 contiguous bytes of one dense row), accumulated in
-//    order, and flushed wherever the next position starts a new row.  Each
-//    staged nonzero is one 16-byte LDS entry (column checked against K once,
-//    value bits, row mark), so a position costs one LDS read and 32-bit
-//    address arithmetic.  Empty rows are written as zeros.
+//  * gather_tiles: a work-group takes a tile of consecutive ranges (tiles
+//    are spread over the XCDs in runs of consecutive tiles, so neighbours
+//    share an L2).  It stages the tile's nonzeros in LDS in one round of
+//    loads: per position the byte offset of its dense row (or a sentinel
+//    past the dense operand for an invalid column), the value bits, and a
+//    row-end mark.  Each wavefront finds the row holding the tile's first
+//    position by a multiway search over rowptr, overlapping the staging
+//    loads; the work-group then marks the last position of every row that
+//    ends in the tile.  Each lane group streams its range in order: batches
+//    of 4 positions, two in flight, each position one raw buffer load of
+//    16 bytes per lane (the buffer range check returns zeros for the
+//    sentinel, so no position needs address arithmetic or a select), fp32
+//    FMAs, and a flush of the accumulated row at each row-end mark.
 //  * A short row (at most R/2 nonzeros) is summed entirely by the lane group
 //    of the range where it starts (running on into the next range, staged as
 //    a halo); the next range skips it.  So every such row is one
 //    sequential fp32 sum, and only longer rows are split: they leave one fp32
 //    partial per range in the workspace ("tail" in the range where they
 //    start, "head" in every later range) and their id in the range's tail
-//    entry; the post pass adds the partials in range order.
+//    entry.
+//  * gather_post adds those partials in range order and writes empty rows
+//    as zeros.
 #include "common.h"
 #include "lanevec.h"
 
@@ -62,11 +64,13 @@ constexpr int kBatch = SPMM_GATHER_BATCH;  // dense rows per batch
 // 18 * 256 positions (16 + 1 ranges of R <= 256), so its loads are all in
 // flight together.
 constexpr int kStageUnroll = 18;
-// A row is "short" (summed by one lane group, never split) when it holds at
-// most R / SPMM_GATHER_SHORT_DIV nonzeros.
+// Dense rows of at least this many bytes are split into column chunks on
+// separate work-groups (and so separate XCDs).
 #ifndef SPMM_GATHER_SPLIT_BYTES
 #define SPMM_GATHER_SPLIT_BYTES 512
 #endif
+// A row is "short" (summed by one lane group, never split) when it holds at
+// most R / SPMM_GATHER_SHORT_DIV nonzeros.
 #ifndef SPMM_GATHER_SHORT_DIV
 #define SPMM_GATHER_SHORT_DIV 2
 #endif
