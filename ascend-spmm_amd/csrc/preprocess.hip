@@ -159,23 +159,50 @@ __global__ void check_rowptr(const I* __restrict__ rowptr, int64_t nrows, int64_
 
 // Expands rows: for element e (position p = p_begin + e) records its row and
 // 64-bit column, checking column range and (optionally) ascending order.
+// Element-parallel, so a row of any length costs the same per element: each
+// work-group takes kExpandChunk consecutive positions, two of its threads
+// bracket the chunk's rows with binary searches over the whole row pointer,
+// and every thread then searches only that bracket (empty when the chunk lies
+// inside one long row).  The row pointer was checked monotone beforehand.
+constexpr int64_t kExpandChunk = 4 * kT;
+
+template <typename I>
+__device__ inline int64_t row_of_position(const I* __restrict__ rowptr, int64_t lo, int64_t hi, int64_t p) {
+  // largest r in [lo, hi] with rowptr[r] <= p (rowptr[lo] <= p holds)
+  while (lo < hi) {
+    const int64_t mid = lo + (hi - lo + 1) / 2;
+    if (static_cast<int64_t>(rowptr[mid]) <= p) lo = mid;
+    else hi = mid - 1;
+  }
+  return lo;
+}
+
 template <typename I>
 __global__ void expand_rows(const I* __restrict__ rowptr, const I* __restrict__ col, int64_t nrows,
-                            int64_t ncols, int64_t p_begin, int64_t* __restrict__ row_of,
+                            int64_t ncols, int64_t p_begin, int64_t n, int64_t* __restrict__ row_of,
                             int64_t* __restrict__ col64, int check_sorted, int* __restrict__ err) {
-  GRID_STRIDE(r, nrows) {
-    const int64_t a = static_cast<int64_t>(rowptr[r]), b = static_cast<int64_t>(rowptr[r + 1]);
-    int64_t prev = -1;
+  __shared__ int64_t bracket[2];
+  const int64_t chunks = (n + kExpandChunk - 1) / kExpandChunk;
+  for (int64_t k = blockIdx.x; k < chunks; k += gridDim.x) {
+    const int64_t e0 = k * kExpandChunk;
+    const int64_t e1 = e0 + kExpandChunk < n ? e0 + kExpandChunk : n;
+    if (threadIdx.x < 2)
+      bracket[threadIdx.x] = row_of_position(rowptr, 0, nrows - 1, p_begin + (threadIdx.x ? e1 - 1 : e0));
+    __syncthreads();
+    const int64_t r_lo = bracket[0], r_hi = bracket[1];
     int bad = 0;
-    for (int64_t p = a; p < b; ++p) {
+    for (int64_t e = e0 + threadIdx.x; e < e1; e += blockDim.x) {
+      const int64_t p = p_begin + e;
+      const int64_t r = row_of_position(rowptr, r_lo, r_hi, p);
       const int64_t c = static_cast<int64_t>(col[p]);
-      row_of[p - p_begin] = r;
-      col64[p - p_begin] = c;
+      row_of[e] = r;
+      col64[e] = c;
       if (c < 0 || c >= ncols) bad |= kBadColumn;
-      if (check_sorted && c < prev) bad |= kUnsortedRow;
-      prev = c;
+      if (check_sorted && p > static_cast<int64_t>(rowptr[r]) && c < static_cast<int64_t>(col[p - 1]))
+        bad |= kUnsortedRow;
     }
     if (bad) atomicOr(err, bad);
+    __syncthreads();
   }
 }
 
@@ -311,6 +338,17 @@ __global__ void gather_counts(const int64_t* __restrict__ order, const int64_t* 
   GRID_STRIDE(i, nb + 1) cnt_sorted[i] = i < nb ? blk_cnt[order[i]] : 0;
 }
 
+// Minimum over the wave, then one atomicMin per wave: a grid of candidates
+// would otherwise serialise on the one address.  Every lane of the wave must
+// call it (after its grid-stride loop); ~0 means "no candidate".
+__device__ inline void wave_atomic_min(unsigned long long* dst, unsigned long long v) {
+  for (int o = 32; o > 0; o >>= 1) {
+    const unsigned long long u = __shfl_xor(v, o);
+    v = u < v ? u : v;
+  }
+  if ((threadIdx.x & 63) == 0 && v != ~0ull) atomicMin(dst, v);
+}
+
 __device__ inline uint64_t nonneg_bits(double d) {
   // Non-negative doubles order like their bit patterns; NaN is never chosen.
   if (!(d >= 0.0)) return 0x7ff0000000000000ull;  // +inf
@@ -328,16 +366,23 @@ __device__ inline double split_diff(int64_t k, int64_t nb, const int64_t* prefix
 
 __global__ void split_min(const int64_t* __restrict__ prefix, int64_t nb, double a,
                           unsigned long long* __restrict__ best) {
-  GRID_STRIDE(k, nb + 1) atomicMin(best, static_cast<unsigned long long>(nonneg_bits(split_diff(k, nb, prefix, a))));
+  unsigned long long m = ~0ull;
+  GRID_STRIDE(k, nb + 1) {
+    const unsigned long long v = nonneg_bits(split_diff(k, nb, prefix, a));
+    m = v < m ? v : m;
+  }
+  wave_atomic_min(best, m);
 }
 
 __global__ void split_first(const int64_t* __restrict__ prefix, int64_t nb, double a,
                             const unsigned long long* __restrict__ best,
                             unsigned long long* __restrict__ kbest) {
+  const unsigned long long target = *best;
+  unsigned long long m = ~0ull;
   GRID_STRIDE(k, nb + 1) {
-    if (nonneg_bits(split_diff(k, nb, prefix, a)) == *best)
-      atomicMin(kbest, static_cast<unsigned long long>(k));
+    if (m == ~0ull && nonneg_bits(split_diff(k, nb, prefix, a)) == target) m = static_cast<unsigned long long>(k);
   }
+  wave_atomic_min(kbest, m);
 }
 
 // Moved blocks: the first k* of the count order (k* = 0 when no finite minimum).
@@ -417,11 +462,13 @@ __global__ void gather_i64(const int64_t* __restrict__ src, const int64_t* __res
 __global__ void boundary_search(const int64_t* __restrict__ snb, const int64_t* __restrict__ snnz,
                                 const int64_t* __restrict__ pnb, const int64_t* __restrict__ pnnz,
                                 int64_t nwin, int64_t nnz, unsigned long long* __restrict__ bpos) {
+  unsigned long long m = ~0ull;
   GRID_STRIDE(pos, nwin) {
     const double aic_after = static_cast<double>(pnb[pos] + snb[pos]) / 295.0;
     const double aiv_after = static_cast<double>(nnz - pnnz[pos] - snnz[pos]) / 505.0;
-    if (aic_after >= aiv_after) atomicMin(bpos, static_cast<unsigned long long>(pos));
+    if (m == ~0ull && aic_after >= aiv_after) m = static_cast<unsigned long long>(pos);
   }
+  wave_atomic_min(bpos, m);
 }
 
 // Scalars shared by the taskmapping kernels (device resident).
@@ -502,22 +549,28 @@ __device__ inline void marginal_cost(const TaskState* s, int64_t q, const int64_
 __global__ void marginal_min(TaskState* __restrict__ s, const int64_t* __restrict__ assigned, int64_t nb) {
   if (s->bwin < 0) return;
   const int64_t c = s->bblocks;
+  unsigned long long m = ~0ull;
   GRID_STRIDE(q, c + 1) {
     double aic, aiv, mx;
     marginal_cost(s, q, assigned, aic, aiv, mx);
-    atomicMin(&s->best_bits, static_cast<unsigned long long>(nonneg_bits(mx)));
+    const unsigned long long v = nonneg_bits(mx);
+    m = v < m ? v : m;
   }
+  wave_atomic_min(&s->best_bits, m);
   (void)nb;
 }
 
 __global__ void marginal_first(TaskState* __restrict__ s, const int64_t* __restrict__ assigned) {
   if (s->bwin < 0) return;
   const int64_t c = s->bblocks;
+  const unsigned long long target = s->best_bits;
+  unsigned long long m = ~0ull;
   GRID_STRIDE(q, c + 1) {
     double aic, aiv, mx;
     marginal_cost(s, q, assigned, aic, aiv, mx);
-    if (nonneg_bits(mx) == s->best_bits) atomicMin(&s->best_q, static_cast<unsigned long long>(q));
+    if (m == ~0ull && nonneg_bits(mx) == target) m = static_cast<unsigned long long>(q);
   }
+  wave_atomic_min(&s->best_q, m);
 }
 
 __global__ void marginal_finish(TaskState* __restrict__ s, const int64_t* __restrict__ assigned,
@@ -871,9 +924,10 @@ spmm_status run_window_sort(const Csr& c, int64_t W, bool check_sorted, WinSort&
   S.p_begin = static_cast<int64_t>(ends[0]);
   S.n = static_cast<int64_t>(ends[1]) - S.p_begin;
 
-  if (c.rows > 0)
-    launch(expand_rows<I>, c.rows, s, static_cast<const I*>(c.rowptr), static_cast<const I*>(c.col),
-           c.rows, c.cols, S.p_begin, S.row_of, S.col64, check_sorted ? 1 : 0, S.err);
+  if (c.rows > 0 && S.n > 0)
+    launch(expand_rows<I>, (S.n + kExpandChunk - 1) / kExpandChunk * kT, s,
+           static_cast<const I*>(c.rowptr), static_cast<const I*>(c.col), c.rows, c.cols, S.p_begin, S.n,
+           S.row_of, S.col64, check_sorted ? 1 : 0, S.err);
   launch(window_keys, S.n, s, S.row_of, S.col64, S.n, W, c.cols, S.key, S.elem);
   if (spmm_status st = check_launch("window_keys")) return st;
   const uint64_t maxkey = static_cast<uint64_t>(S.nwin > 0 ? S.nwin : 1) * static_cast<uint64_t>(c.cols > 0 ? c.cols : 1);

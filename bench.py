@@ -6,14 +6,17 @@ N=128 fp16, fp32 accumulate) — the configuration the headline metric
 A step is one SpMM call over resident device inputs.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 2] [--width N]
-                       [--op csr|mixed|mixed-empty|bcsr|graph] [--no-cpu] [--no-block-path] [--no-cold]
+                       [--op csr|mixed|mixed-empty|bcsr|graph|preprocess] [--no-cpu] [--no-block-path] [--no-cold]
        python bench.py --copy-calibration
 
 ``--op mixed`` times ``spmm_ascend_cube`` on the output of the GPU
 ``preprocess`` (block windows on MFMA, the rest on the gather path); ``--op
 bcsr`` on the output of ``csr_to_bcsr`` (every window on MFMA); ``--op
 graph`` times pack_node_tensor -> spmm_ascend_cube on P A P^T ->
-restore_node_tensor (``preprocess(graph_layout=True)``).  Unless
+restore_node_tensor (``preprocess(graph_layout=True)``).  ``--op preprocess``
+times the GPU preprocessing pipelines themselves (csr_to_bcsr,
+block_level_split, preprocess) against the oracle's C restatement of the
+reference's host routines.  Unless
 ``--no-block-path`` is given, the line also carries ``block_path``: config 3
 (block-banded) at N=128 fp16, ``spmm_ascend_cube`` against ``spmm_csr`` on the
 same matrix.  ``--copy-calibration`` runs a plain 256 MiB device copy five
@@ -232,6 +235,83 @@ def block_path(spmm_npu, dev, steps: int, warmup: int) -> dict:
     }
 
 
+def preprocessing(spmm_npu, w, steps: int, warmup: int, cpu: bool) -> int:
+    """--op preprocess: the GPU preprocessing pipelines (csr_to_bcsr,
+    csr_to_ascend_cube, block_level_split with the harness ratio (222/190)/2, preprocess; the
+    graph layout for config 5) on device-resident CSR, wall time per call
+    (each pipeline synchronises once to size its outputs), against the
+    oracle's single-threaded C restatement of the reference's host routines
+    on the same matrix (extension/custom_op.cpp:594-746, 429-592, 1146-1348,
+    765-1110).
+    Bytes per call: the CSR read (int32 indices) plus every output written."""
+    dev = torch.device("cuda:0")
+    crow, col, val = device_csr(w, dev)
+    graph = w.name.startswith("C5")
+    ratio = (222.0 / 190.0) * 0.5
+    pipelines = {
+        "csr_to_bcsr": lambda: spmm_npu.csr_to_bcsr(crow, col, val, w.rows, w.cols, 16),
+        "csr_to_ascend_cube": lambda: spmm_npu.csr_to_ascend_cube(crow, col, val, w.rows, w.cols, 16),
+        "block_level_split": lambda: spmm_npu.block_level_split(crow, col, val, w.rows, w.cols, ratio, 16),
+        "preprocess": lambda: spmm_npu.preprocess(crow, col, val, w.rows, w.cols, 16, graph),
+    }
+    in_bytes = 4 * (w.rows + 1) + (4 + w.values.itemsize) * w.nnz
+    out = {}
+    for name, fn in pipelines.items():
+        res = fn()
+        torch.cuda.synchronize()
+        out_bytes = sum(t.numel() * t.element_size() for t in res.values() if torch.is_tensor(t))
+        del res
+        wall_ms, _ = time_calls(fn, steps, warmup)
+        out[name] = {"ms": round(wall_ms, 3), "bytes": int(in_bytes + out_bytes),
+                     "gbps": round((in_bytes + out_bytes) / (wall_ms / 1e3) / 1e9, 1)}
+        log(f"[bench] {name}: {wall_ms:.3f} ms")
+    cpu_out = None
+    if cpu:
+        sys.path.insert(0, os.path.join(REPO, "oracle"))
+        import oracle  # checker-only import: the CPU baseline leg
+
+        c32, k32 = w.crow.astype(np.int32), w.col.astype(np.int32)
+        cpu_fns = {
+            "csr_to_bcsr": lambda: oracle.csr_to_bcsr(c32, k32, w.values, w.rows, w.cols, 16),
+            "csr_to_ascend_cube": lambda: oracle.csr_to_ascend_cube(c32, k32, w.values, w.rows, w.cols, 16),
+            "block_level_split": lambda: oracle.block_level_split(c32, k32, w.values, w.rows, w.cols, ratio, 16),
+            "preprocess": lambda: oracle.preprocess(c32, k32, w.values, w.rows, w.cols, 16, graph),
+        }
+        cpu_out = {}
+        for name, fn in cpu_fns.items():
+            t0 = time.perf_counter()
+            fn()
+            cpu_out[name] = round((time.perf_counter() - t0) * 1e3, 1)
+            out[name]["cpu_ms"] = cpu_out[name]
+            out[name]["speedup_vs_cpu"] = round(cpu_out[name] / out[name]["ms"], 1)
+            log(f"[bench] oracle {name}: {cpu_out[name]:.1f} ms")
+    pre = out["preprocess"]
+    result = {
+        "metric": "GPU preprocessing throughput (nnz per second of preprocess)",
+        "value": round(w.nnz / (pre["ms"] / 1e3) / 1e6, 2),
+        "unit": "Mnnz/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": pre["ms"],
+        "higher_is_better": True,
+        "data": "synthetic (seeded generator of benchmark configuration %s)" % w.name[1],
+        "config": {"workload": f"{w.name} {w.rows}x{w.cols} nnz={w.nnz} {w.dtype}",
+                   "op": "preprocess" + (" (graph layout)" if graph else ""), "index": "int32"},
+        "roofline": {"bound": "hbm", "achieved": pre["gbps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(pre["gbps"] / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "bytes_per_call": pre["bytes"]},
+        "pipelines": out,
+        "cpu_baseline": None if cpu_out is None else {
+            "value": round(w.nnz / (cpu_out["preprocess"] / 1e3) / 1e6, 2), "unit": "Mnnz/s", "cores": 1,
+            "kind": "port",
+            "sample": "full matrix, one call of the oracle's C restatement of the reference's "
+                      "single-threaded host routine"},
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def copy_calibration() -> int:
     n = 256 * 1024 * 1024
     src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
@@ -249,7 +329,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", type=int, default=2)
     ap.add_argument("--width", type=int, default=None)
-    ap.add_argument("--op", choices=["csr", "mixed", "mixed-empty", "bcsr", "graph"], default="csr")
+    ap.add_argument("--op", choices=["csr", "mixed", "mixed-empty", "bcsr", "graph", "preprocess"], default="csr")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-block-path", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
@@ -269,6 +349,8 @@ def main() -> int:
     import spmm_npu
 
     w = workloads.make(args.config)
+    if args.op == "preprocess":
+        return preprocessing(spmm_npu, w, min(args.steps, 10), min(args.warmup, 2), not args.no_cpu)
     width = args.width or w.widths[0]
     B = w.dense(width)
     log(f"[bench] workload {w.name}: {w.rows}x{w.cols}, nnz={w.nnz}, N={width}, {w.dtype}")
