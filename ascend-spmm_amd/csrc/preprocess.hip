@@ -29,7 +29,9 @@
 #include <rocprim/device/device_radix_sort.hpp>
 #include <rocprim/device/device_scan.hpp>
 
+#include <algorithm>
 #include <cmath>
+#include <cstdint>
 #include <string>
 
 #include "common.h"
@@ -130,6 +132,10 @@ __global__ void fill_kernel(T* __restrict__ p, int64_t n, T v) {
 
 __global__ void fill_bytes(unsigned char* __restrict__ p, int64_t n) {
   GRID_STRIDE(i, n) p[i] = 0;
+}
+
+__global__ void fill_zero16(uint4* __restrict__ p, int64_t n) {
+  GRID_STRIDE(i, n) p[i] = make_uint4(0u, 0u, 0u, 0u);
 }
 
 // dst[i] = src[i] converted to the output index type.
@@ -338,15 +344,26 @@ __global__ void gather_counts(const int64_t* __restrict__ order, const int64_t* 
   GRID_STRIDE(i, nb + 1) cnt_sorted[i] = i < nb ? blk_cnt[order[i]] : 0;
 }
 
-// Minimum over the wave, then one atomicMin per wave: a grid of candidates
-// would otherwise serialise on the one address.  Every lane of the wave must
-// call it (after its grid-stride loop); ~0 means "no candidate".
-__device__ inline void wave_atomic_min(unsigned long long* dst, unsigned long long v) {
+// Grid-wide minima.  Same-address device-scope atomics serialise (measured
+// about 11 ns apiece on MI355X, so one per wave made a 1.9M-candidate minimum
+// take 0.33 ms): the kernels that use this run a grid capped at kReduceGroups
+// work-groups whose threads loop, reduce over the work-group, and issue one
+// atomicMin per work-group.  Every thread of the work-group must call it;
+// ~0 means "no candidate".
+constexpr unsigned kReduceGroups = 512;
+
+__device__ inline void group_atomic_min(unsigned long long* dst, unsigned long long v) {
+  __shared__ unsigned long long part[kT / 64];
   for (int o = 32; o > 0; o >>= 1) {
     const unsigned long long u = __shfl_xor(v, o);
     v = u < v ? u : v;
   }
-  if ((threadIdx.x & 63) == 0 && v != ~0ull) atomicMin(dst, v);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = v;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < kT / 64; ++w) v = part[w] < v ? part[w] : v;
+    if (v != ~0ull) atomicMin(dst, v);
+  }
 }
 
 __device__ inline uint64_t nonneg_bits(double d) {
@@ -371,7 +388,7 @@ __global__ void split_min(const int64_t* __restrict__ prefix, int64_t nb, double
     const unsigned long long v = nonneg_bits(split_diff(k, nb, prefix, a));
     m = v < m ? v : m;
   }
-  wave_atomic_min(best, m);
+  group_atomic_min(best, m);
 }
 
 __global__ void split_first(const int64_t* __restrict__ prefix, int64_t nb, double a,
@@ -382,7 +399,7 @@ __global__ void split_first(const int64_t* __restrict__ prefix, int64_t nb, doub
   GRID_STRIDE(k, nb + 1) {
     if (m == ~0ull && nonneg_bits(split_diff(k, nb, prefix, a)) == target) m = static_cast<unsigned long long>(k);
   }
-  wave_atomic_min(kbest, m);
+  group_atomic_min(kbest, m);
 }
 
 // Moved blocks: the first k* of the count order (k* = 0 when no finite minimum).
@@ -468,7 +485,7 @@ __global__ void boundary_search(const int64_t* __restrict__ snb, const int64_t* 
     const double aiv_after = static_cast<double>(nnz - pnnz[pos] - snnz[pos]) / 505.0;
     if (m == ~0ull && aic_after >= aiv_after) m = static_cast<unsigned long long>(pos);
   }
-  wave_atomic_min(bpos, m);
+  group_atomic_min(bpos, m);
 }
 
 // Scalars shared by the taskmapping kernels (device resident).
@@ -556,7 +573,7 @@ __global__ void marginal_min(TaskState* __restrict__ s, const int64_t* __restric
     const unsigned long long v = nonneg_bits(mx);
     m = v < m ? v : m;
   }
-  wave_atomic_min(&s->best_bits, m);
+  group_atomic_min(&s->best_bits, m);
   (void)nb;
 }
 
@@ -570,7 +587,7 @@ __global__ void marginal_first(TaskState* __restrict__ s, const int64_t* __restr
     marginal_cost(s, q, assigned, aic, aiv, mx);
     if (m == ~0ull && nonneg_bits(mx) == target) m = static_cast<unsigned long long>(q);
   }
-  wave_atomic_min(&s->best_q, m);
+  group_atomic_min(&s->best_q, m);
 }
 
 __global__ void marginal_finish(TaskState* __restrict__ s, const int64_t* __restrict__ assigned,
@@ -823,6 +840,13 @@ inline void launch(K kernel, int64_t n, hipStream_t s, Args... args) {
   hipLaunchKernelGGL(kernel, dim3(grid_for(n)), dim3(kT), 0, s, args...);
 }
 
+// Launch of a kernel that ends in group_atomic_min (capped grid).
+template <typename K, typename... Args>
+inline void launch_reduce(K kernel, int64_t n, hipStream_t s, Args... args) {
+  const unsigned g = grid_for(n);
+  hipLaunchKernelGGL(kernel, dim3(g < kReduceGroups ? g : kReduceGroups), dim3(kT), 0, s, args...);
+}
+
 struct Csr {
   int64_t rows, cols, nnz;
   int32_t it, vt;
@@ -900,9 +924,17 @@ spmm_status read_back(T* host, const T* dev, int64_t count, hipStream_t s) {
   return check_hip(e, "reading preprocessing results");
 }
 
+// Zeroes `bytes` bytes at p: 16-byte stores over the aligned body, byte
+// stores for the unaligned head and the tail.
 spmm_status zero(void* p, int64_t bytes, hipStream_t s) {
   if (bytes <= 0) return SPMM_OK;
-  launch(fill_bytes, bytes, s, static_cast<unsigned char*>(p), bytes);
+  unsigned char* b = static_cast<unsigned char*>(p);
+  const int64_t head = std::min<int64_t>(bytes, (16 - reinterpret_cast<uintptr_t>(b) % 16) % 16);
+  const int64_t body = (bytes - head) / 16;
+  const int64_t tail = bytes - head - 16 * body;
+  if (head) launch(fill_bytes, head, s, b, head);
+  if (body) launch(fill_zero16, body, s, reinterpret_cast<uint4*>(b + head), body);
+  if (tail) launch(fill_bytes, tail, s, b + head + 16 * body, tail);
   return check_launch("zero fill");
 }
 
@@ -1098,8 +1130,8 @@ spmm_status hybrid_run(const Csr& c, double a, int64_t W, HybridArrays& H, Ctx& 
   launch(gather_counts, nb + 1, s, H.corder, S.blk_cnt, nb, H.cnt_sorted);
   if (hipError_t e = x.prims.exclusive_sum(H.cnt_sorted, H.prefix, nb + 1)) return check_hip(e, "prefix");
   launch(fill_kernel<unsigned long long>, 2, s, H.best, int64_t(2), ~0ull);
-  launch(split_min, nb + 1, s, H.prefix, nb, a, H.best);
-  launch(split_first, nb + 1, s, H.prefix, nb, a, H.best, H.best + 1);
+  launch_reduce(split_min, nb + 1, s, H.prefix, nb, a, H.best);
+  launch_reduce(split_first, nb + 1, s, H.prefix, nb, a, H.best, H.best + 1);
   launch(mark_moved, nb, s, H.corder, nb, H.best, H.best + 1, H.kept);
   launch(fill_kernel<int64_t>, 1, s, H.kept + nb, int64_t(1), int64_t(0));
   if (hipError_t e = x.prims.exclusive_sum(H.kept, H.kscan, nb + 1)) return check_hip(e, "kept scan");
@@ -1278,15 +1310,15 @@ spmm_status task_plan(const Csr& c, bool graph_layout, void* ws, size_t ws_bytes
   if (hipError_t e = x.prims.exclusive_sum(A.snnz, A.pnnz, nwin)) return check_hip(e, "nnz prefix");
   // Marginal window and its block split (custom_op.cpp:813-885).
   launch(task_init, 1, s, A.st);
-  launch(boundary_search, nwin, s, A.snb, A.snnz, A.pnb, A.pnnz, nwin, c.nnz, &A.st->bpos);
+  launch_reduce(boundary_search, nwin, s, A.snb, A.snnz, A.pnb, A.pnnz, nwin, c.nnz, &A.st->bpos);
   launch(task_marginal, 1, s, A.st, A.swin, A.snb, A.snnz, A.pnb, A.pnnz, c.nnz);
   launch(marginal_keys, nb, s, A.st, S.win_start, S.blk_first, S.blk_cnt, nb, A.mkey, A.mid, S.err);
   if (hipError_t e = x.prims.sort_pairs(A.mkey, A.smkey, A.mid, A.morder, nb, 64))
     return check_hip(e, "marginal sort");
   launch(marginal_occ, nb + 1, s, A.morder, S.blk_cnt, A.st, nb, A.occ);
   if (hipError_t e = x.prims.exclusive_sum(A.occ, A.assigned, nb + 1)) return check_hip(e, "assigned");
-  launch(marginal_min, nb + 1, s, A.st, A.assigned, nb);
-  launch(marginal_first, nb + 1, s, A.st, A.assigned);
+  launch_reduce(marginal_min, nb + 1, s, A.st, A.assigned, nb);
+  launch_reduce(marginal_first, nb + 1, s, A.st, A.assigned);
   launch(marginal_finish, 1, s, A.st, A.assigned, nwin);
   launch(marginal_to_aic, nb, s, A.st, A.morder, nb, A.to_aic);
   // Window roles, rows and permutation (custom_op.cpp:887-940).
