@@ -10,25 +10,26 @@
 //    gathered dense rows are B (K x N).  fp16 uses v_mfma_f32_16x16x32_f16
 //    (K-step 32 blocks), fp32 uses v_mfma_f32_16x16x4_f32 (K-step 4 blocks).
 //  * Dense gather without an LDS transpose: lane (q = lane % 16, kg = lane / 16)
-//    loads, for each of its K-step blocks, 4 consecutive columns
-//    n0 + 4q .. n0 + 4q + 3 of the block's dense row (one 8-byte load for
-//    fp16, 16 bytes for fp32; 16 lanes read 128/256 contiguous bytes).  MFMA j
-//    (j = 0..3) takes element j of each load, so its B column q is the dense
-//    column n0 + 4q + j.  Four MFMAs therefore cover a 64-column group and
-//    the accumulator lane holds 4 consecutive output columns.
+//    loads, for each of its K-step blocks, C consecutive columns
+//    n0 + C*q .. n0 + C*q + C-1 of the block's dense row in one load (fp16:
+//    C = 4, 8 bytes, or C = 8, 16 bytes, for outputs of 256 columns or more;
+//    fp32: C = 4, 16 bytes).  MFMA j (j < C) takes element j of each load, so
+//    its B column q is the dense column n0 + C*q + j.  C MFMAs therefore
+//    cover a column group of 16*C columns and the accumulator lane holds C
+//    consecutive output columns.  An output element's MFMA sequence is the
+//    same for either C.
 //  * A work-group first stages its chunk's block columns and values in LDS
 //    (coalesced 16-byte loads); the A fragment A[r][k] = Cvalue[16*(b0+k) + r]
 //    is then read from LDS in the [block][row] layout the reference's
-//    converters produce.  The dense rows of the next K-step are loaded while
-//    the current one is multiplied, and the accumulators are finished (plus
-//    the vector sums, rounded once) straight from registers.
-//  * Waves of the work-group take 64-column groups round-robin; each group
+//    converters produce.  Each K-step issues all of its dense loads before
+//    its MFMAs, and the accumulators are finished (plus the vector sums,
+//    rounded once) straight from registers.
+//  * Waves of the work-group take column groups round-robin; each group
 //    runs the whole K loop, so every output element sees the same MFMA
 //    sequence for every width N.
-//  * Windows longer than a chunk (block_chunk_for: 512 blocks fp16, 256
+//  * Windows longer than a chunk (block_chunk_for: 2048 blocks fp16, 1024
 //    fp32, growing with the total block count) are cut at fixed block
-//    positions: the window's own work-group
-//    takes its first chunk, and "overflow" work-groups take the rest in fixed
+//    positions: the window's own work-group takes its first chunk, and "overflow" work-groups take the rest in fixed
 //    global block ranges (only one window can overflow into a range).  A
 //    combine kernel adds the pieces in order, so the split is deterministic.
 //  * Vector (CSR) nonzeros of rows inside block windows are summed by the CSR
@@ -59,7 +60,7 @@ typedef float float4_t __attribute__((ext_vector_type(4)));
 #define SPMM_BLOCK_XCD_RUN 16
 #endif
 constexpr int64_t kBlockXcdRun = SPMM_BLOCK_XCD_RUN;
-// Waves per window work-group: one per 64-column group, up to this many (the
+// Waves per window work-group: one per column group, up to this many (the
 // rest loop), so wide outputs do not lengthen each wave's chain of K-steps.
 #ifndef SPMM_BLOCK_MAX_WAVES
 #define SPMM_BLOCK_MAX_WAVES 4
@@ -135,55 +136,73 @@ __device__ inline unsigned stage_chunk(const BlockArgs<T, I>& a, int64_t s, bool
   return s_vec;
 }
 
-// One K-step of dense rows per lane, loaded before the step is multiplied.
-// Lanes of padding blocks or blocks with an invalid column get zeros (never a
-// load), so they contribute exactly nothing.
-template <typename T> struct StepRows;
-template <> struct StepRows<_Float16> {  // 8 blocks x 4 columns per lane (K-step 32)
-  half4_t r[8];
-};
-template <> struct StepRows<float> {  // 4 blocks x 4 columns per lane (K-step 16)
-  float4_t r[4];
-};
+// Columns a lane holds, C: 4 (an 8-byte fp16 piece or a 16-byte fp32 piece
+// of a dense row) or 8 (a 16-byte fp16 piece).  Sixteen lanes cover a column
+// group of 16 * C columns, and a K-step runs C MFMAs, one per column of the
+// piece.  fp16 takes C = 8 for outputs of at least 256 columns (two or more
+// waves per window); narrower outputs keep C = 4, so a window still has two
+// waves at N = 128 (work-groups per CU are bounded by their LDS staging).
+// The MFMA sequence of an output element does not depend on C.
+template <int C>
+using half_c = _Float16 __attribute__((ext_vector_type(C)));
+template <typename T>
+constexpr int lane_cols_for(int64_t N) { return sizeof(T) == 2 && N >= 256 ? 8 : 4; }
 
-// MFMA sum of staged blocks [0, n) for the 64-column group at n0.  Lane
-// (q = lane % 16, kg = lane / 16) loads columns n0+4q .. n0+4q+3 of its
-// blocks' dense rows; MFMA j uses element j, so the accumulator lane holds 4
-// consecutive output columns (rows 4kg .. 4kg+3).  Adds to `acc`.
-template <typename T, typename I>
+template <typename T, int C>
+__device__ inline void store_cols(T* p, const float* v) {
+  if constexpr (sizeof(T) == 2) {
+    half_c<C> h;
+#pragma unroll
+    for (int i = 0; i < C; ++i) h[i] = static_cast<_Float16>(v[i]);
+    *reinterpret_cast<half_c<C>*>(p) = h;
+  } else {
+    *reinterpret_cast<float4_t*>(p) = float4_t{v[0], v[1], v[2], v[3]};
+  }
+}
+
+// MFMA sum of staged blocks [0, n) for the column group at n0.  Lane
+// (q = lane % 16, kg = lane / 16) loads columns n0 + C*q .. n0 + C*q + C-1
+// of its blocks' dense rows with one load per block (16 lanes read
+// 16 * C * sizeof(T) contiguous bytes); MFMA j takes element j of each load,
+// so its B column q is the dense column n0 + C*q + j and the accumulator lane
+// holds C consecutive output columns of rows 4kg .. 4kg+3.  Lanes of padding
+// blocks or blocks with an invalid column get zeros (never a load), so they
+// contribute exactly nothing.  Adds to `acc`.
+template <typename T, typename I, int C>
 __device__ inline void group_sum(const BlockArgs<T, I>& a, const uint32_t* s_col, const T* s_val,
-                                 int64_t n, int64_t n0, int lane, float4_t (&acc)[4]) {
+                                 int64_t n, int64_t n0, int lane, float4_t (&acc)[C]) {
+  static_assert(C == 4 || (C == 8 && sizeof(T) == 2), "lane columns: 4, or 8 for fp16");
   const int q = lane & 15, kg = lane >> 4;
-  const bool col_ok = (n0 + 4 * q) < a.N;
-  const T* dense_q = a.dense + n0 + 4 * q;
+  const bool col_ok = (n0 + C * q) < a.N;  // N % C == 0: the piece is wholly inside or outside
+  const T* dense_q = a.dense + n0 + C * q;
   const uint32_t Nu = static_cast<uint32_t>(a.N);
   if (a.K <= 0 || n <= 0) return;  // uniform: no valid dense row
   const int32_t steps = static_cast<int32_t>((n + k_step<T>() - 1) / k_step<T>());
   if constexpr (sizeof(T) == 2) {
     for (int32_t st = 0; st < steps; ++st) {
-      const int32_t k0 = st * 32 + 8 * kg;
-      StepRows<_Float16> rows;
+      const int32_t k0 = st * 32 + 8 * kg;  // this lane's 8 blocks of the 32-block step
+      half_c<C> rows[8];
       half8_t av;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const uint32_t c = s_col[k0 + e];
         av[e] = s_val[(k0 + e) * 16 + q];
         if (col_ok && c != kBadCol)
-          rows.r[e] = *reinterpret_cast<const half4_t*>(dense_q + static_cast<uint64_t>(c) * Nu);
+          rows[e] = *reinterpret_cast<const half_c<C>*>(dense_q + static_cast<uint64_t>(c) * Nu);
         else
-          rows.r[e] = half4_t{0, 0, 0, 0};
+          rows[e] = half_c<C>(static_cast<_Float16>(0));
       }
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < C; ++j) {
         half8_t b;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) b[e] = rows.r[e][j];
+        for (int e = 0; e < 8; ++e) b[e] = rows[e][j];
         acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b, acc[j], 0, 0, 0);
       }
     }
   } else {
     for (int32_t st = 0; st < steps; ++st) {
-      StepRows<float> rows;
+      float4_t rows[4];
       float av[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
@@ -191,15 +210,15 @@ __device__ inline void group_sum(const BlockArgs<T, I>& a, const uint32_t* s_col
         const uint32_t c = s_col[blk];
         av[u] = s_val[blk * 16 + q];
         if (col_ok && c != kBadCol)
-          rows.r[u] = *reinterpret_cast<const float4_t*>(dense_q + static_cast<uint64_t>(c) * Nu);
+          rows[u] = *reinterpret_cast<const float4_t*>(dense_q + static_cast<uint64_t>(c) * Nu);
         else
-          rows.r[u] = float4_t{0.f, 0.f, 0.f, 0.f};
+          rows[u] = float4_t{0.f, 0.f, 0.f, 0.f};
       }
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[u], rows.r[u][j], acc[j], 0, 0, 0);
+          acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[u], rows[u][j], acc[j], 0, 0, 0);
       }
     }
   }
@@ -223,7 +242,7 @@ __device__ inline unsigned window_vector_rows(const BlockArgs<T, I>& a, int64_t 
 // sum goes to that [16][N] workspace slot instead.  Blocks are staged in LDS
 // `a.stage` at a time (a multiple of the K-step, so the MFMA sequence does
 // not depend on it); a window that fits is staged once for all column groups.
-template <typename T, typename I>
+template <typename T, typename I, int C>
 __device__ inline void window_chunk(const BlockArgs<T, I>& a, int64_t s, int64_t b0, int64_t b1,
                                     float* slot, uint32_t* s_col, T* s_val) {
   const int64_t n = b1 - b0;
@@ -233,51 +252,53 @@ __device__ inline void window_chunk(const BlockArgs<T, I>& a, int64_t s, int64_t
     vec = stage_chunk(a, s, slot == nullptr, b0, b1, s_col, s_val);
   else if (slot == nullptr)
     vec = window_vector_rows(a, s);
+  constexpr int64_t kGroupCols = 16 * C;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int waves = blockDim.x >> 6;
   const int q = lane & 15, kg = lane >> 4;
-  const int64_t groups = (a.N + 63) / 64;
+  const int64_t groups = (a.N + kGroupCols - 1) / kGroupCols;
   // Uniform trip count over the work-group (staging synchronises it).
   for (int64_t gbase = 0; gbase < groups; gbase += waves) {
     const int64_t g = gbase + wave;
     const bool active = g < groups;
-    const int64_t n0 = 64 * g;
-    float4_t acc[4];
+    const int64_t n0 = kGroupCols * g;
+    float4_t acc[C];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[j] = float4_t{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < C; ++j) acc[j] = float4_t{0.f, 0.f, 0.f, 0.f};
     if (once) {
-      if (active) group_sum(a, s_col, s_val, n, n0, lane, acc);
+      if (active) group_sum<T, I, C>(a, s_col, s_val, n, n0, lane, acc);
     } else {
       for (int64_t sb = 0; sb < n; sb += a.stage) {
         const int64_t m = n - sb < a.stage ? n - sb : a.stage;
         __syncthreads();  // the previous piece is no longer read
         stage_chunk(a, s, false, b0 + sb, b0 + sb + m, s_col, s_val);
-        if (active) group_sum(a, s_col, s_val, m, n0, lane, acc);
+        if (active) group_sum<T, I, C>(a, s_col, s_val, m, n0, lane, acc);
       }
     }
-    const int64_t c0 = n0 + 4 * q;
+    const int64_t c0 = n0 + C * q;
     if (!active || c0 >= a.N) continue;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int r = 4 * kg + e;
-      float v[4] = {acc[0][e], acc[1][e], acc[2][e], acc[3][e]};
+      float v[C];
+#pragma unroll
+      for (int j = 0; j < C; ++j) v[j] = acc[j][e];
       if (slot) {
-        *reinterpret_cast<float4_t*>(slot + r * a.N + c0) = float4_t{v[0], v[1], v[2], v[3]};
+#pragma unroll
+        for (int w = 0; w < C; w += 4)
+          *reinterpret_cast<float4_t*>(slot + r * a.N + c0 + w) = float4_t{v[w], v[w + 1], v[w + 2], v[w + 3]};
         continue;
       }
       const int64_t row = 16 * s + r;
       if (vec >> r & 1u) {
-        const float4_t p = *reinterpret_cast<const float4_t*>(a.vpart + row * a.N + c0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = v[i] + p[i];
+        for (int w = 0; w < C; w += 4) {
+          const float4_t p = *reinterpret_cast<const float4_t*>(a.vpart + row * a.N + c0 + w);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) v[w + i] = v[w + i] + p[i];
+        }
       }
-      if constexpr (sizeof(T) == 2) {
-        *reinterpret_cast<half4_t*>(a.out + row * a.N + c0) =
-            half4_t{static_cast<_Float16>(v[0]), static_cast<_Float16>(v[1]),
-                    static_cast<_Float16>(v[2]), static_cast<_Float16>(v[3])};
-      } else {
-        *reinterpret_cast<float4_t*>(a.out + row * a.N + c0) = float4_t{v[0], v[1], v[2], v[3]};
-      }
+      store_cols<T, C>(a.out + row * a.N + c0, v);
     }
   }
 }
@@ -288,12 +309,16 @@ __device__ inline void window_chunk(const BlockArgs<T, I>& a, int64_t s, int64_t
 // Work-groups 8*per_xcd + k: overflow range k = blocks [k*kbig, (k+1)*kbig).
 // Only the window holding block k*kbig can have blocks past its first chunk
 // in that range; that segment's sum goes to slot (k, 0).
-template <typename T, typename I>
 #ifndef SPMM_BLOCK_WAVES
 #define SPMM_BLOCK_WAVES 4
 #endif
-// Waves per SIMD the register budget of block_windows is fitted to.
-__global__ __launch_bounds__(64 * kMaxWaves) __attribute__((amdgpu_waves_per_eu(SPMM_BLOCK_WAVES))) void block_windows(BlockArgs<T, I> a) {
+#ifndef SPMM_BLOCK_WAVES_WIDE
+#define SPMM_BLOCK_WAVES_WIDE 4
+#endif
+// Waves per SIMD the register budget of block_windows is fitted to (C = 8
+// holds twice the accumulators and dense pieces).
+template <typename T, typename I, int C>
+__global__ __launch_bounds__(64 * kMaxWaves) __attribute__((amdgpu_waves_per_eu(C == 8 ? SPMM_BLOCK_WAVES_WIDE : SPMM_BLOCK_WAVES))) void block_windows(BlockArgs<T, I> a) {
   extern __shared__ __align__(16) unsigned char smem[];
   T* s_val = reinterpret_cast<T*>(smem);                           // [stage][16]
   uint32_t* s_col = reinterpret_cast<uint32_t*>(smem + a.stage * 16 * sizeof(T));  // [stage]
@@ -309,7 +334,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) __attribute__((amdgpu_waves_per_eu(
     if (b1 <= b0) return;  // empty window: rows handled by the vector pass
     const bool single = b1 - b0 <= a.kbig;
     if (!single) b1 = b0 + a.kbig;
-    window_chunk(a, s, b0, b1, single ? nullptr : a.slots + (2 * ((b0 + a.kbig) / a.kbig) + 1) * n16,
+    window_chunk<T, I, C>(a, s, b0, b1, single ? nullptr : a.slots + (2 * ((b0 + a.kbig) / a.kbig) + 1) * n16,
                  s_col, s_val);
     return;
   }
@@ -330,7 +355,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) __attribute__((amdgpu_waves_per_eu(
   const int64_t lo = b0 + a.kbig > bk ? b0 + a.kbig : bk;
   const int64_t hi = b1 < bk + a.kbig ? b1 : bk + a.kbig;
   if (lo >= hi) return;
-  window_chunk(a, s, lo, hi, a.slots + (2 * k) * n16, s_col, s_val);
+  window_chunk<T, I, C>(a, s, lo, hi, a.slots + (2 * k) * n16, s_col, s_val);
 }
 
 // Combine pass, one work-group per (overflow range k, slice of 4*256 fp32
@@ -408,7 +433,8 @@ spmm_status block_typed(const void* Crowptr, const void* Ccol, const void* Cvalu
   a.noverflow = block_overflow_ranges(a.limit, a.kbig);
   a.first_of = reinterpret_cast<int64_t*>(slots + a.noverflow * 2 * 16 * N);
   a.per_xcd = ceil_div(windows, kXcds * kBlockXcdRun) * kBlockXcdRun;
-  const int64_t groups = (N + 63) / 64;
+  const int C = lane_cols_for<T>(N);
+  const int64_t groups = ceil_div(N, 16 * C);
   const int waves = groups < kMaxWaves ? static_cast<int>(groups) : kMaxWaves;
   // Staging piece: about twice the mean window, 64 blocks up to a 20 KB LDS
   // budget (512 blocks fp16, 256 fp32), so LDS per work-group stays small for
@@ -419,8 +445,9 @@ spmm_status block_typed(const void* Crowptr, const void* Ccol, const void* Cvalu
   while (a.stage < 2 * mean && a.stage < a.kbig && a.stage < stage_max) a.stage *= 2;
   const size_t stage_lds = static_cast<size_t>(a.stage) * (16 * sizeof(T) + sizeof(uint32_t));
   const int64_t grid = a.per_xcd * kXcds + a.noverflow;
-  hipLaunchKernelGGL((block_windows<T, I>), dim3(static_cast<unsigned>(grid)), dim3(64 * waves),
-                     stage_lds, stream, a);
+  constexpr int kWide = sizeof(T) == 2 ? 8 : 4;  // fp32 only has C = 4
+  auto kernel = C == 8 ? block_windows<T, I, kWide> : block_windows<T, I, 4>;
+  hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(grid)), dim3(64 * waves), stage_lds, stream, a);
   if (spmm_status st = check_launch("block_windows")) return st;
   if (a.noverflow == 0) return SPMM_OK;
   const int64_t slices = ceil_div(16 * N, kCombineSlice);
