@@ -21,9 +21,12 @@
 //  * A work-group first stages its chunk's block columns and values in LDS
 //    (coalesced 16-byte loads); the A fragment A[r][k] = Cvalue[16*(b0+k) + r]
 //    is then read from LDS in the [block][row] layout the reference's
-//    converters produce.  Each K-step issues all of its dense loads before
-//    its MFMAs, and the accumulators are finished (plus the vector sums,
-//    rounded once) straight from registers.
+//    converters produce.  Dense pieces are raw buffer loads whose range
+//    check turns an invalid or padding block into zeros (no branches; dense
+//    operands past 4 GB use 64-bit global loads with selects).  With C = 4
+//    the next K-step's loads are issued before the current step's MFMAs, and
+//    the accumulators are finished (plus the vector sums, rounded once)
+//    straight from registers.
 //  * Waves of the work-group take column groups round-robin; each group
 //    runs the whole K loop, so every output element sees the same MFMA
 //    sequence for every width N.
@@ -42,6 +45,19 @@
 #include "common.h"
 #include "lanevec.h"
 #include "wgsearch.h"
+
+#include <type_traits>
+
+// Raw buffer loads of 8 and 16 bytes (the LLVM AMDGPU intrinsics): address =
+// the resource's base + voffset + soffset, with the resource's range check (a
+// load whose offset is past the extent returns zeros).
+typedef int spmm_block_rsrc_t __attribute__((ext_vector_type(4)));
+typedef int spmm_block_i2_t __attribute__((ext_vector_type(2)));
+typedef int spmm_block_i4_t __attribute__((ext_vector_type(4)));
+__device__ spmm_block_i2_t spmm_block_buffer_load_b64(spmm_block_rsrc_t rsrc, uint32_t voffset, uint32_t soffset,
+                                                      int32_t aux) __asm("llvm.amdgcn.raw.buffer.load.v2i32");
+__device__ spmm_block_i4_t spmm_block_buffer_load_b128(spmm_block_rsrc_t rsrc, uint32_t voffset, uint32_t soffset,
+                                                       int32_t aux) __asm("llvm.amdgcn.raw.buffer.load.v4i32");
 
 namespace spmm {
 namespace {
@@ -94,37 +110,107 @@ struct BlockArgs {
   __device__ inline bool row_has_vector(int64_t r) const { return r < vrows && vrp(r) != vrp(r + 1); }
 };
 
-constexpr uint32_t kBadCol = 0xFFFFFFFFu;  // staged column id of an invalid block
-
 // K-step of the MFMA loop: blocks per step (fp16 16x16x32 takes 8 blocks per
 // lane group of 16 lanes, fp32 16x16x4 takes 4).
 template <typename T>
 constexpr int64_t k_step() { return sizeof(T) == 2 ? 32 : 16; }
 
-// LDS staging of one chunk of blocks [b0, b1) (b1 - b0 <= stage): the block
-// columns, checked against K here once (kBadCol when out of range), and the
-// 16 values of every block, loaded with coalesced 16-byte pieces (Cvalue is
+// Columns a lane holds, C: 4 (an 8-byte fp16 piece or a 16-byte fp32 piece
+// of a dense row) or 8 (a 16-byte fp16 piece).  Sixteen lanes cover a column
+// group of 16 * C columns, and a K-step runs C MFMAs, one per column of the
+// piece.  fp16 takes C = 8 for outputs of at least 256 columns (two or more
+// waves per window); narrower outputs keep C = 4, so a window still has two
+// waves at N = 128.  The MFMA sequence of an output element does not depend
+// on C.
+template <int C>
+using half_c = _Float16 __attribute__((ext_vector_type(C)));
+template <typename T>
+constexpr int lane_cols_for(int64_t N) { return sizeof(T) == 2 && N >= 256 ? 8 : 4; }
+
+// The piece of a dense row one lane loads per block.
+template <typename T, int C>
+using Piece = typename std::conditional<sizeof(T) == 2, half_c<C>, float4_t>::type;
+
+// Dense-piece loaders.  Each stages a 32-bit source per block (in LDS, once
+// per chunk) and turns it into the lane's piece of that dense row, or zeros
+// for an invalid block column or a padding block.  A lane whose columns lie
+// past N reads columns 0 .. C-1 of the same rows instead: MFMA output column
+// q depends on B column q only, and those output columns are never stored.
+//
+// BlockBufferLoader (dense operands up to kBlockBufferLimit bytes): the
+// source is the row's byte offset col * N * sizeof(T), read with a raw buffer
+// load whose extent is the dense operand; an invalid block stages
+// kBlockBufferNone, which with any lane offset (< 4096) lies past the extent,
+// so the buffer range check returns zeros without a memory access.  No
+// branches and no per-block address arithmetic.
+constexpr uint32_t kBlockBufferNone = 0xFFFFF000u;
+constexpr int64_t kBlockBufferLimit = kBlockBufferNone;
+
+template <typename T, int C>
+struct BlockBufferLoader {
+  spmm_block_rsrc_t rsrc;
+  uint32_t lane_bytes;
+  static constexpr uint32_t kNone = kBlockBufferNone;
+  __device__ inline BlockBufferLoader(const T* dense, int64_t K, int64_t N, int64_t col0) {
+    const uint64_t p = reinterpret_cast<uint64_t>(dense);
+    rsrc[0] = static_cast<int>(p & 0xFFFFFFFFu);
+    rsrc[1] = static_cast<int>((p >> 32) & 0xFFFFu);  // stride 0: raw buffer
+    rsrc[2] = static_cast<int>(static_cast<uint32_t>(K * N * static_cast<int64_t>(sizeof(T))));
+    rsrc[3] = 0x00020000;  // 32-bit data format; no swizzle, no thread-id offset
+    lane_bytes = static_cast<uint32_t>(col0 * static_cast<int64_t>(sizeof(T)));
+  }
+  __device__ static inline uint32_t stage(int64_t c, int64_t K, int64_t N) {
+    return static_cast<uint64_t>(c) < static_cast<uint64_t>(K)
+               ? static_cast<uint32_t>(c) * static_cast<uint32_t>(N * static_cast<int64_t>(sizeof(T)))
+               : kNone;
+  }
+  __device__ inline Piece<T, C> load(uint32_t src) const {
+    if constexpr (sizeof(Piece<T, C>) == 8)
+      return __builtin_bit_cast(Piece<T, C>, spmm_block_buffer_load_b64(rsrc, src + lane_bytes, 0u, 0));
+    else
+      return __builtin_bit_cast(Piece<T, C>, spmm_block_buffer_load_b128(rsrc, src + lane_bytes, 0u, 0));
+  }
+};
+
+// BlockGlobalLoader (larger dense operands): the source is the column id, or
+// kBadCol; an invalid block loads dense row 0 (K >= 1 here) and uses zeros.
+constexpr uint32_t kBadCol = 0xFFFFFFFFu;
+
+template <typename T, int C>
+struct BlockGlobalLoader {
+  const T* dense_c;  // dense + the lane's first column
+  uint32_t N;
+  static constexpr uint32_t kNone = kBadCol;
+  __device__ inline BlockGlobalLoader(const T* dense, int64_t, int64_t n, int64_t col0)
+      : dense_c(dense + col0), N(static_cast<uint32_t>(n)) {}
+  __device__ static inline uint32_t stage(int64_t c, int64_t K, int64_t) {
+    return static_cast<uint64_t>(c) < static_cast<uint64_t>(K) ? static_cast<uint32_t>(c) : kNone;
+  }
+  __device__ inline Piece<T, C> load(uint32_t src) const {
+    const bool ok = src != kNone;
+    const Piece<T, C> x = *reinterpret_cast<const Piece<T, C>*>(dense_c + static_cast<uint64_t>(ok ? src : 0u) * N);
+    return ok ? x : Piece<T, C>(static_cast<T>(0));
+  }
+};
+
+// LDS staging of one chunk of blocks [b0, b1) (b1 - b0 <= stage): the
+// loader's source per block column, checked against K here once, and the 16
+// values of every block, loaded with coalesced 16-byte pieces (Cvalue is
 // 16-byte aligned by contract).  The chunk is padded to a whole K-step with
-// kBadCol columns and zero values, so the MFMA loop reads LDS without bounds
+// invalid sources and zero values, so the MFMA loop reads LDS without bounds
 // checks.  With `finish` set it also returns the window's vector-row bits
 // (bit r: row 16*s + r has vector-part nonzeros, whose fp32 sum is in vpart),
 // read in the same round trip.
-template <typename T, typename I>
+template <typename T, typename I, typename Loader>
 __device__ inline unsigned stage_chunk(const BlockArgs<T, I>& a, int64_t s, bool finish, int64_t b0,
-                                       int64_t b1, uint32_t* s_col, T* s_val) {
+                                       int64_t b1, uint32_t* s_src, T* s_val) {
   __shared__ unsigned s_vec;
   const int64_t n = b1 - b0;
   const int64_t n_pad = (n + k_step<T>() - 1) / k_step<T>() * k_step<T>();
   if (threadIdx.x == 0) s_vec = 0;
   const bool vec = finish && threadIdx.x < 16 && a.row_has_vector(16 * s + threadIdx.x);
-  for (int64_t i = threadIdx.x; i < n_pad; i += blockDim.x) {
-    uint32_t c = kBadCol;
-    if (i < n) {
-      const int64_t cv = static_cast<int64_t>(a.Ccol[b0 + i]);
-      c = static_cast<uint64_t>(cv) < static_cast<uint64_t>(a.K) ? static_cast<uint32_t>(cv) : kBadCol;
-    }
-    s_col[i] = c;
-  }
+  for (int64_t i = threadIdx.x; i < n_pad; i += blockDim.x)
+    s_src[i] = i < n ? Loader::stage(static_cast<int64_t>(a.Ccol[b0 + i]), a.K, a.N) : Loader::kNone;
   constexpr int64_t kPer = 16 * sizeof(T) / 16;  // 16-byte pieces per block
   const lanes::raw16_t* src = reinterpret_cast<const lanes::raw16_t*>(a.Cvalue + 16 * b0);
   lanes::raw16_t* dst = reinterpret_cast<lanes::raw16_t*>(s_val);
@@ -135,18 +221,6 @@ __device__ inline unsigned stage_chunk(const BlockArgs<T, I>& a, int64_t s, bool
   __syncthreads();
   return s_vec;
 }
-
-// Columns a lane holds, C: 4 (an 8-byte fp16 piece or a 16-byte fp32 piece
-// of a dense row) or 8 (a 16-byte fp16 piece).  Sixteen lanes cover a column
-// group of 16 * C columns, and a K-step runs C MFMAs, one per column of the
-// piece.  fp16 takes C = 8 for outputs of at least 256 columns (two or more
-// waves per window); narrower outputs keep C = 4, so a window still has two
-// waves at N = 128 (work-groups per CU are bounded by their LDS staging).
-// The MFMA sequence of an output element does not depend on C.
-template <int C>
-using half_c = _Float16 __attribute__((ext_vector_type(C)));
-template <typename T>
-constexpr int lane_cols_for(int64_t N) { return sizeof(T) == 2 && N >= 256 ? 8 : 4; }
 
 template <typename T, int C>
 __device__ inline void store_cols(T* p, const float* v) {
@@ -160,67 +234,86 @@ __device__ inline void store_cols(T* p, const float* v) {
   }
 }
 
+// One K-step of one lane: its dense pieces (kPieces blocks) and A values.
+template <typename T, int C>
+struct StepOperands {
+  static constexpr int kPieces = sizeof(T) == 2 ? 8 : 4;
+  Piece<T, C> x[kPieces];
+  typename std::conditional<sizeof(T) == 2, half8_t, float4_t>::type av;
+};
+
 // MFMA sum of staged blocks [0, n) for the column group at n0.  Lane
 // (q = lane % 16, kg = lane / 16) loads columns n0 + C*q .. n0 + C*q + C-1
 // of its blocks' dense rows with one load per block (16 lanes read
 // 16 * C * sizeof(T) contiguous bytes); MFMA j takes element j of each load,
 // so its B column q is the dense column n0 + C*q + j and the accumulator lane
-// holds C consecutive output columns of rows 4kg .. 4kg+3.  Lanes of padding
-// blocks or blocks with an invalid column get zeros (never a load), so they
-// contribute exactly nothing.  Adds to `acc`.
-template <typename T, typename I, int C>
-__device__ inline void group_sum(const BlockArgs<T, I>& a, const uint32_t* s_col, const T* s_val,
+// holds C consecutive output columns of rows 4kg .. 4kg+3.  With C = 4 the
+// loads of the next K-step are issued before the current step's MFMAs (two
+// steps of operands in registers).  Adds to `acc`.
+template <typename T, typename I, int C, typename Loader>
+__device__ inline void group_sum(const BlockArgs<T, I>& a, const uint32_t* s_src, const T* s_val,
                                  int64_t n, int64_t n0, int lane, float4_t (&acc)[C]) {
   static_assert(C == 4 || (C == 8 && sizeof(T) == 2), "lane columns: 4, or 8 for fp16");
   const int q = lane & 15, kg = lane >> 4;
-  const bool col_ok = (n0 + C * q) < a.N;  // N % C == 0: the piece is wholly inside or outside
-  const T* dense_q = a.dense + n0 + C * q;
-  const uint32_t Nu = static_cast<uint32_t>(a.N);
+  const int64_t col0 = n0 + C * q < a.N ? n0 + C * q : 0;  // N % C == 0
+  const Loader ld(a.dense, a.K, a.N, col0);
   if (a.K <= 0 || n <= 0) return;  // uniform: no valid dense row
   const int32_t steps = static_cast<int32_t>((n + k_step<T>() - 1) / k_step<T>());
-  if constexpr (sizeof(T) == 2) {
-    for (int32_t st = 0; st < steps; ++st) {
-      const int32_t k0 = st * 32 + 8 * kg;  // this lane's 8 blocks of the 32-block step
-      half_c<C> rows[8];
-      half8_t av;
+
+  // fp16: the lane's 8 blocks of a 32-block step are consecutive (8kg ..);
+  // fp32: its 4 blocks of a 16-block step are kg, kg+4, kg+8, kg+12.
+  auto fetch = [&](StepOperands<T, C>& o, int32_t st) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint32_t c = s_col[k0 + e];
-        av[e] = s_val[(k0 + e) * 16 + q];
-        if (col_ok && c != kBadCol)
-          rows[e] = *reinterpret_cast<const half_c<C>*>(dense_q + static_cast<uint64_t>(c) * Nu);
-        else
-          rows[e] = half_c<C>(static_cast<_Float16>(0));
-      }
+    for (int e = 0; e < StepOperands<T, C>::kPieces; ++e) {
+      const int32_t blk = sizeof(T) == 2 ? st * 32 + 8 * kg + e : st * 16 + 4 * e + kg;
+      o.av[e] = s_val[blk * 16 + q];
+      o.x[e] = ld.load(s_src[blk]);
+    }
+  };
+  auto multiply = [&](const StepOperands<T, C>& o) {
+    if constexpr (sizeof(T) == 2) {
 #pragma unroll
       for (int j = 0; j < C; ++j) {
         half8_t b;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) b[e] = rows[e][j];
-        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b, acc[j], 0, 0, 0);
+        for (int e = 0; e < 8; ++e) b[e] = o.x[e][j];
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(o.av, b, acc[j], 0, 0, 0);
       }
-    }
-  } else {
-    for (int32_t st = 0; st < steps; ++st) {
-      float4_t rows[4];
-      float av[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int32_t blk = st * 16 + 4 * u + kg;
-        const uint32_t c = s_col[blk];
-        av[u] = s_val[blk * 16 + q];
-        if (col_ok && c != kBadCol)
-          rows[u] = *reinterpret_cast<const float4_t*>(dense_q + static_cast<uint64_t>(c) * Nu);
-        else
-          rows[u] = float4_t{0.f, 0.f, 0.f, 0.f};
-      }
+    } else {
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[u], rows[u][j], acc[j], 0, 0, 0);
+          acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(o.av[u], o.x[u][j], acc[j], 0, 0, 0);
       }
     }
+  };
+  if constexpr (C == 8) {
+    // Twice the operands per step: one step in registers (two would halve
+    // the waves per SIMD).
+    for (int32_t st = 0; st < steps; ++st) {
+      StepOperands<T, C> A;
+      fetch(A, st);
+      multiply(A);
+    }
+    return;
+  }
+  StepOperands<T, C> A, B;
+  fetch(A, 0);
+  int32_t st = 0;
+  for (; st + 3 <= steps; st += 2) {
+    fetch(B, st + 1);
+    multiply(A);
+    fetch(A, st + 2);
+    multiply(B);
+  }
+  // A holds step st; one or two steps remain.
+  if (st + 2 == steps) {
+    fetch(B, st + 1);
+    multiply(A);
+    multiply(B);
+  } else {
+    multiply(A);
   }
 }
 
@@ -242,14 +335,14 @@ __device__ inline unsigned window_vector_rows(const BlockArgs<T, I>& a, int64_t 
 // sum goes to that [16][N] workspace slot instead.  Blocks are staged in LDS
 // `a.stage` at a time (a multiple of the K-step, so the MFMA sequence does
 // not depend on it); a window that fits is staged once for all column groups.
-template <typename T, typename I, int C>
+template <typename T, typename I, int C, typename Loader>
 __device__ inline void window_chunk(const BlockArgs<T, I>& a, int64_t s, int64_t b0, int64_t b1,
                                     float* slot, uint32_t* s_col, T* s_val) {
   const int64_t n = b1 - b0;
   const bool once = n <= a.stage;
   unsigned vec = 0;
   if (once)
-    vec = stage_chunk(a, s, slot == nullptr, b0, b1, s_col, s_val);
+    vec = stage_chunk<T, I, Loader>(a, s, slot == nullptr, b0, b1, s_col, s_val);
   else if (slot == nullptr)
     vec = window_vector_rows(a, s);
   constexpr int64_t kGroupCols = 16 * C;
@@ -266,13 +359,13 @@ __device__ inline void window_chunk(const BlockArgs<T, I>& a, int64_t s, int64_t
 #pragma unroll
     for (int j = 0; j < C; ++j) acc[j] = float4_t{0.f, 0.f, 0.f, 0.f};
     if (once) {
-      if (active) group_sum<T, I, C>(a, s_col, s_val, n, n0, lane, acc);
+      if (active) group_sum<T, I, C, Loader>(a, s_col, s_val, n, n0, lane, acc);
     } else {
       for (int64_t sb = 0; sb < n; sb += a.stage) {
         const int64_t m = n - sb < a.stage ? n - sb : a.stage;
         __syncthreads();  // the previous piece is no longer read
-        stage_chunk(a, s, false, b0 + sb, b0 + sb + m, s_col, s_val);
-        if (active) group_sum<T, I, C>(a, s_col, s_val, m, n0, lane, acc);
+        stage_chunk<T, I, Loader>(a, s, false, b0 + sb, b0 + sb + m, s_col, s_val);
+        if (active) group_sum<T, I, C, Loader>(a, s_col, s_val, m, n0, lane, acc);
       }
     }
     const int64_t c0 = n0 + C * q;
@@ -317,7 +410,7 @@ __device__ inline void window_chunk(const BlockArgs<T, I>& a, int64_t s, int64_t
 #endif
 // Waves per SIMD the register budget of block_windows is fitted to (C = 8
 // holds twice the accumulators and dense pieces).
-template <typename T, typename I, int C>
+template <typename T, typename I, int C, typename Loader>
 __global__ __launch_bounds__(64 * kMaxWaves) __attribute__((amdgpu_waves_per_eu(C == 8 ? SPMM_BLOCK_WAVES_WIDE : SPMM_BLOCK_WAVES))) void block_windows(BlockArgs<T, I> a) {
   extern __shared__ __align__(16) unsigned char smem[];
   T* s_val = reinterpret_cast<T*>(smem);                           // [stage][16]
@@ -334,7 +427,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) __attribute__((amdgpu_waves_per_eu(
     if (b1 <= b0) return;  // empty window: rows handled by the vector pass
     const bool single = b1 - b0 <= a.kbig;
     if (!single) b1 = b0 + a.kbig;
-    window_chunk<T, I, C>(a, s, b0, b1, single ? nullptr : a.slots + (2 * ((b0 + a.kbig) / a.kbig) + 1) * n16,
+    window_chunk<T, I, C, Loader>(a, s, b0, b1, single ? nullptr : a.slots + (2 * ((b0 + a.kbig) / a.kbig) + 1) * n16,
                  s_col, s_val);
     return;
   }
@@ -355,7 +448,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) __attribute__((amdgpu_waves_per_eu(
   const int64_t lo = b0 + a.kbig > bk ? b0 + a.kbig : bk;
   const int64_t hi = b1 < bk + a.kbig ? b1 : bk + a.kbig;
   if (lo >= hi) return;
-  window_chunk<T, I, C>(a, s, lo, hi, a.slots + (2 * k) * n16, s_col, s_val);
+  window_chunk<T, I, C, Loader>(a, s, lo, hi, a.slots + (2 * k) * n16, s_col, s_val);
 }
 
 // Combine pass, one work-group per (overflow range k, slice of 4*256 fp32
@@ -446,7 +539,12 @@ spmm_status block_typed(const void* Crowptr, const void* Ccol, const void* Cvalu
   const size_t stage_lds = static_cast<size_t>(a.stage) * (16 * sizeof(T) + sizeof(uint32_t));
   const int64_t grid = a.per_xcd * kXcds + a.noverflow;
   constexpr int kWide = sizeof(T) == 2 ? 8 : 4;  // fp32 only has C = 4
-  auto kernel = C == 8 ? block_windows<T, I, kWide> : block_windows<T, I, 4>;
+  // Dense operands within a 32-bit byte extent use buffer loads.
+  const bool buffer = K * N * static_cast<int64_t>(sizeof(T)) <= kBlockBufferLimit;
+  auto kernel = buffer ? (C == 8 ? block_windows<T, I, kWide, BlockBufferLoader<T, kWide>>
+                                 : block_windows<T, I, 4, BlockBufferLoader<T, 4>>)
+                       : (C == 8 ? block_windows<T, I, kWide, BlockGlobalLoader<T, kWide>>
+                                 : block_windows<T, I, 4, BlockGlobalLoader<T, 4>>);
   hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(grid)), dim3(64 * waves), stage_lds, stream, a);
   if (spmm_status st = check_launch("block_windows")) return st;
   if (a.noverflow == 0) return SPMM_OK;

@@ -469,6 +469,59 @@ def test_dense_operand_beyond_32bit_extent(spmm_npu):
     torch.cuda.empty_cache()
 
 
+@pytest.mark.parametrize("dtype,N", [("fp32", 512), ("fp16", 1024)])
+def test_block_part_dense_beyond_32bit_extent(spmm_npu, dtype, N):
+    """The block kernel on a dense operand larger than 4 GB (K = 2.2M rows)
+    takes its 64-bit global-load path (fp32: 4-column pieces; fp16 at
+    N = 1024: 8-column pieces); blocks in the last rows of B and an invalid
+    block column (contributes zero) are included."""
+    K, rows = 2_200_000, 200
+    tdt = torch.float32 if dtype == "fp32" else torch.float16
+    rng = np.random.default_rng(79)
+    B = torch.empty((K, N), dtype=tdt, device="cuda")
+    B.normal_(generator=torch.Generator(device="cuda").manual_seed(6))
+    assert K * N * B.element_size() > 0xFFFFF000
+    deg = rng.integers(0, 40, rows)
+    crow = np.zeros(rows + 1, np.int64)
+    crow[1:] = np.cumsum(deg)
+    col = np.concatenate([np.sort(rng.choice(K, d, replace=False)) for d in deg]).astype(np.int64)
+    col[: deg[0]] = np.sort(rng.choice(np.arange(K - 500, K), deg[0], replace=False))  # the far end of B
+    vals = rng.uniform(-1, 1, col.size).astype(NP_DT[dtype])
+    b = O.csr_to_bcsr(crow, col, vals, rows, K, 16)
+    ucol = b["unique_col_ids"].copy()
+    ucol[3] = K + 7  # one invalid block column
+    i32 = torch.int32
+    out = spmm_npu.spmm_ascend_cube(
+        dev(b["crow_window_ptr"], i32), dev(ucol, i32), dev(b["value"]), zero_start(1),
+        torch.zeros(0, dtype=i32, device="cuda"), torch.zeros(0, dtype=tdt, device="cuda"), B,
+        dev(O.make_start(b["crow_window_ptr"], 20)), zero_start(40))
+    # Expected: the blocks as a CSR over the used dense rows (the invalid block's
+    # 16 values dropped), in fp64.
+    nwin = b["crow_window_ptr"].size - 1
+    bcol = ucol.astype(np.int64)
+    blk_rows, blk_cols, blk_vals = [], [], []
+    for s in range(nwin):
+        for k in range(int(b["crow_window_ptr"][s]), int(b["crow_window_ptr"][s + 1])):
+            if bcol[k] >= K:
+                continue
+            for r in range(16):
+                blk_rows.append(16 * s + r)
+                blk_cols.append(bcol[k])
+                blk_vals.append(b["value"][16 * k + r])
+    blk_rows = np.asarray(blk_rows)
+    order = np.lexsort((np.asarray(blk_cols), blk_rows))
+    ecrow = np.zeros(16 * nwin + 1, np.int64)
+    np.add.at(ecrow, blk_rows + 1, 1)
+    ecrow = np.cumsum(ecrow)
+    ecol = np.asarray(blk_cols)[order]
+    evals = np.asarray(blk_vals)[order]
+    used = np.unique(ecol)
+    Bsub = B[torch.from_numpy(used).cuda()].cpu().numpy()
+    assert_close(out, O.spmm_f64(ecrow, np.searchsorted(used, ecol), evals, Bsub), dtype)
+    del B
+    torch.cuda.empty_cache()
+
+
 @pytest.mark.parametrize("dtype,width", [("fp16", 64), ("fp16", 512), ("fp32", 64), ("fp32", 512)])
 def test_windows_longer_than_the_block_chunk(spmm_npu, dtype, width):
     """Windows of thousands of 16x1 blocks are cut into chunks summed by
