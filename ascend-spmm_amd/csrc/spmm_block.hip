@@ -101,6 +101,7 @@ struct BlockArgs {
   int64_t* first_of;       // [noverflow]: window whose blocks past its first chunk start in range k, or -1
   int64_t kbig, noverflow, per_xcd;
   int64_t stage;           // blocks staged in LDS at a time (multiple of the K-step)
+  int zero_empty;          // no vector part: windows without blocks write their rows as zeros
 
   __device__ inline int64_t crp(int64_t s) const { return clampi(static_cast<int64_t>(Crowptr[s]), 0, limit); }
   __device__ inline int64_t vrp(int64_t r) const {
@@ -424,7 +425,14 @@ __global__ __launch_bounds__(64 * kMaxWaves) __attribute__((amdgpu_waves_per_eu(
     if (s >= a.windows) return;  // uniform over the work-group
     const int64_t b0 = a.crp(s);
     int64_t b1 = a.crp(s + 1);
-    if (b1 <= b0) return;  // empty window: rows handled by the vector pass
+    if (b1 <= b0) {  // empty window: its rows are the vector pass's, or zeros
+      if (a.zero_empty) {
+        lanes::raw16_t* dst = reinterpret_cast<lanes::raw16_t*>(a.out + 16 * s * a.N);
+        const int64_t pieces = n16 * static_cast<int64_t>(sizeof(T)) / 16;
+        for (int64_t i = threadIdx.x; i < pieces; i += blockDim.x) dst[i] = lanes::raw16_t{0u, 0u, 0u, 0u};
+      }
+      return;
+    }
     const bool single = b1 - b0 <= a.kbig;
     if (!single) b1 = b0 + a.kbig;
     window_chunk<T, I, C, Loader>(a, s, b0, b1, single ? nullptr : a.slots + (2 * ((b0 + a.kbig) / a.kbig) + 1) * n16,
@@ -522,6 +530,7 @@ spmm_status block_typed(const void* Crowptr, const void* Ccol, const void* Cvalu
   a.out = static_cast<T*>(out);
   a.vpart = vpart;
   a.slots = slots;
+  a.zero_empty = vector_nnz == 0 ? 1 : 0;
   a.kbig = block_chunk_for(sizeof(T) == 2 ? SPMM_VALUE_F16 : SPMM_VALUE_F32, a.limit);
   a.noverflow = block_overflow_ranges(a.limit, a.kbig);
   a.first_of = reinterpret_cast<int64_t*>(slots + a.noverflow * 2 * 16 * N);

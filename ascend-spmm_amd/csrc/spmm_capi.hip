@@ -192,9 +192,12 @@ spmm_status spmm_mixed_run(const spmm_mixed_desc* d, const void* Crowptr, const 
   float* vpart = lay.vpart > 0 ? reinterpret_cast<float*>(ws + lay.gather) : nullptr;
   float* slots = reinterpret_cast<float*>(ws + lay.gather + lay.vpart);
   // Vector pass first (it leaves the fp32 vector sums of block-window rows in
-  // vpart), then the block part, which adds them and rounds once.
+  // vpart), then the block part, which adds them and rounds once.  Without
+  // vector nonzeros the block kernel writes the zero rows of windows without
+  // blocks itself, and the vector pass only covers rows past the windows.
+  const int64_t row_lo = d->vector_nnz == 0 ? 16 * d->block_windows : 0;
   spmm_status st = launch_gather(d->index_type, d->value_type, Vrowptr, Vcol, Vvalue, d->vector_nnz,
-                                 d->vector_rows, 0, out_rows, dense, d->dense_rows, d->width, out, ws,
+                                 d->vector_rows, row_lo, out_rows, dense, d->dense_rows, d->width, out, ws,
                                  lay.gather, d->block_windows > 0 ? Crowptr : nullptr, d->block_windows,
                                  lay.limit, vpart, s);
   if (st != SPMM_OK) return st;

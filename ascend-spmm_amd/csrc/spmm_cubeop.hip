@@ -195,8 +195,8 @@ spmm_status cube_typed(const spmm_cube_op_desc* d, const void* rowptr_v, const v
     hipLaunchKernelGGL((cube_run_values<T, I>), dim3(pos_blocks), dim3(kThreads), 0, stream, col, value, nnz,
                        run_pos, total, block_value);
   if (spmm_status st = check_launch("spmm_cube decode")) return st;
-  // Block part on the decoded windows; the (empty) vector pass writes zeros
-  // to the rows of windows without blocks.
+  // Block part on the decoded windows (no vector part: the block kernel
+  // writes zeros to the rows of windows without blocks).
   return spmm_mixed_run(&lay.md, crow, run_col, block_value, crow, run_col, block_value, dense, out,
                         ws + lay.mixed, lay.total_bytes - lay.mixed, reinterpret_cast<spmm_stream>(stream));
 }

@@ -127,6 +127,56 @@ def test_direct_cabi_calls_match_oracle(lib):
     assert torch.equal(out.cpu(), out2.cpu())
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("vector_rows", [0, 16 * 6 + 5])
+def test_mixed_block_only_writes_every_row(lib, vector_rows):
+    """Block part only (no vector nonzeros) with windows that have no blocks:
+    every output row is written (the block sums, zeros elsewhere), over an
+    output pre-filled with NaN.  With vector_rows past the block windows, the
+    rows beyond them are written as zeros too."""
+    import torch
+
+    import oracle as O
+
+    rng = np.random.default_rng(8)
+    K, N, windows = 300, 128, 5
+    rows = 16 * windows
+    deg = rng.integers(1, 25, rows)
+    deg[16:32] = 0   # window 1 has no blocks
+    deg[64:80] = 0   # nor the last window
+    crow = np.zeros(rows + 1, np.int64)
+    crow[1:] = np.cumsum(deg)
+    col = np.concatenate([np.sort(rng.choice(K, d, replace=False)) for d in deg]).astype(np.int64)
+    vals = rng.uniform(-1, 1, col.size).astype(np.float16)
+    B = rng.standard_normal((K, N)).astype(np.float16)
+    b = O.csr_to_bcsr(crow, col, vals, rows, K, 16)
+    assert np.diff(b["crow_window_ptr"])[1] == 0 and np.diff(b["crow_window_ptr"])[4] == 0
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    p = lambda x: ctypes.c_void_p(x.data_ptr())
+    i32 = np.int32
+    d_crow, d_ucol, d_val = t(b["crow_window_ptr"].astype(i32)), t(b["unique_col_ids"].astype(i32)), t(b["value"])
+    d_vrow = torch.zeros(vector_rows + 1, dtype=torch.int32, device="cuda")
+    d_B = t(B)
+    m = MixedDesc(windows, b["unique_col_ids"].size, b["value"].size, vector_rows, 0, K, N, 0, 0)
+    out_rows = lib.spmm_mixed_out_rows(ctypes.byref(m))
+    assert out_rows == max(rows, vector_rows)
+    out = torch.full((out_rows, N), float("nan"), dtype=torch.float16, device="cuda")
+    ws_bytes = ctypes.c_size_t(0)
+    assert lib.spmm_mixed_workspace(ctypes.byref(m), ctypes.byref(ws_bytes)) == 0
+    ws = torch.empty(max(ws_bytes.value, 1), dtype=torch.uint8, device="cuda")
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    rc = lib.spmm_mixed_run(ctypes.byref(m), p(d_crow), p(d_ucol), p(d_val), p(d_vrow), None, None,
+                            p(d_B), p(out), p(ws), ctypes.c_size_t(ws_bytes.value), stream)
+    assert rc == 0, lib.spmm_last_error()
+    torch.cuda.synchronize()
+    got = out.cpu().double().numpy()
+    expected = np.zeros((out_rows, N))
+    expected[:rows] = O.spmm_f64(crow, col, vals, B)
+    assert not np.isnan(got).any()
+    assert np.allclose(got, expected, atol=2e-2, rtol=2e-2)
+    assert (got[16:32] == 0).all() and (got[64:] == 0).all()
+
+
 def test_rowscalar_host_validation(lib):
     d = CsrDesc(10, 5, 10, 24, 0, 0)
     assert lib.spmm_csr_rowscalar_run(ctypes.byref(d), None, None, None, None, None, None) == 4
