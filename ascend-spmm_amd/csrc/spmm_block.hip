@@ -347,6 +347,8 @@ __device__ inline void window_chunk(const BlockArgs<T, I>& a, int64_t s, int64_t
   else if (slot == nullptr)
     vec = window_vector_rows(a, s);
   constexpr int64_t kGroupCols = 16 * C;
+  T* const out_w = a.out + 16 * s * a.N;
+  const float* const vpart_w = a.vpart + 16 * s * a.N;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int waves = blockDim.x >> 6;
   const int q = lane & 15, kg = lane >> 4;
@@ -371,28 +373,31 @@ __device__ inline void window_chunk(const BlockArgs<T, I>& a, int64_t s, int64_t
     }
     const int64_t c0 = n0 + C * q;
     if (!active || c0 >= a.N) continue;
+    // Element offsets inside the window's 16 x N tile (< 2^14) from the
+    // window's base pointers, which are uniform: no 64-bit row address per
+    // lane stays live across the column-group loop.
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int r = 4 * kg + e;
+      const uint32_t o = static_cast<uint32_t>(r * a.N + c0);
       float v[C];
 #pragma unroll
       for (int j = 0; j < C; ++j) v[j] = acc[j][e];
       if (slot) {
 #pragma unroll
         for (int w = 0; w < C; w += 4)
-          *reinterpret_cast<float4_t*>(slot + r * a.N + c0 + w) = float4_t{v[w], v[w + 1], v[w + 2], v[w + 3]};
+          *reinterpret_cast<float4_t*>(slot + o + w) = float4_t{v[w], v[w + 1], v[w + 2], v[w + 3]};
         continue;
       }
-      const int64_t row = 16 * s + r;
       if (vec >> r & 1u) {
 #pragma unroll
         for (int w = 0; w < C; w += 4) {
-          const float4_t p = *reinterpret_cast<const float4_t*>(a.vpart + row * a.N + c0 + w);
+          const float4_t p = *reinterpret_cast<const float4_t*>(vpart_w + o + w);
 #pragma unroll
           for (int i = 0; i < 4; ++i) v[w + i] = v[w + i] + p[i];
         }
       }
-      store_cols<T, C>(a.out + row * a.N + c0, v);
+      store_cols<T, C>(out_w + o, v);
     }
   }
 }

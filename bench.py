@@ -312,13 +312,22 @@ def preprocessing(spmm_npu, w, steps: int, warmup: int, cpu: bool) -> int:
     return 0
 
 
-def copy_calibration() -> int:
-    n = 256 * 1024 * 1024
+def copy_gbps(n: int, copies: int, warmup: int) -> tuple:
+    """A plain device copy of n bytes (torch's copy kernel): (ms per copy,
+    read + write GB/s).  At 1 GiB the source and destination (2 GiB) are far
+    past the 256 MB Infinity Cache, so this is the achievable HBM rate."""
     src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
     dst = torch.empty_like(src)
-    _, ms = time_calls(lambda: dst.copy_(src), 5, 0)
+    _, ms = time_calls(lambda: dst.copy_(src), copies, warmup)
+    del src, dst
+    return ms, 2 * n / (ms / 1e3) / 1e9
+
+
+def copy_calibration() -> int:
+    n = 256 * 1024 * 1024
+    ms, gbps = copy_gbps(n, 5, 0)
     print(json.dumps({"copy_bytes": n, "copies": 5, "ms_per_copy": round(ms, 4),
-                      "copy_gbps_read_plus_write": round(2 * n / (ms / 1e3) / 1e9, 1)}), flush=True)
+                      "copy_gbps_read_plus_write": round(gbps, 1)}), flush=True)
     return 0
 
 
@@ -416,6 +425,9 @@ def main() -> int:
         _, cold_ms = time_calls(step, min(args.steps, 10), 1, cold=True)
         log(f"[bench] cold-cache events {cold_ms:.4f} ms/call")
 
+    copy_rate = copy_gbps(1 << 30, 5, 1)[1]
+    log(f"[bench] 1 GiB device copy: {copy_rate:.1f} GB/s (read + write)")
+
     flops = 2.0 * w.nnz * width
     t_s = wall_ms / 1e3
     achieved = alg_bytes / (event_ms / 1e3) / 1e9
@@ -454,6 +466,8 @@ def main() -> int:
             "traffic": traffic,
             "traffic_gbps": None if traffic is None else round(traffic / (event_ms / 1e3) / 1e9, 1),
             "traffic_frac": None if traffic is None else round(traffic / (event_ms / 1e3) / 1e9 / HBM_PEAK_GBPS, 4),
+            "copy_gbps": round(copy_rate, 1),
+            "traffic_frac_of_copy": None if traffic is None else round(traffic / (event_ms / 1e3) / 1e9 / copy_rate, 4),
             "algorithmic_bytes_per_call": alg_bytes,
             "gather_model_bytes": int(w.nnz * width * s_b),
             "event_ms_per_call": round(event_ms, 5),
