@@ -59,9 +59,9 @@ MFMA_PEAK_TFLOPS = {"fp16": 2500.0, "fp32": 157.3}
 FETCH_SCALE = 2.0
 WRITE_SCALE = 1.0
 PMC_KIB = {
-    (2, "csr", 128): {"fetch_kib": 205398.5 + 3879.9, "write_kib": 31384.5 + 659.8},
-    (3, "mixed", 128): {"fetch_kib": 52058.7 + 6313.1 + 131765.5 + 160.0,
-                        "write_kib": 12092.2 + 2266.5 + 14184.4 + 0.0},
+    (2, "csr", 128): {"fetch_kib": 205390.2 + 3879.9, "write_kib": 31384.8 + 659.8},
+    (3, "mixed", 128): {"fetch_kib": 51627.0 + 6313.1 + 131191.3 + 52.6,
+                        "write_kib": 12091.8 + 2266.5 + 14135.5 + 0.0},
 }
 
 def log(msg: str) -> None:
