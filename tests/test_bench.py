@@ -1,0 +1,68 @@
+"""The bench.py contract: one JSON line with the driver's keys plus
+``roofline`` (and ``cpu_baseline`` unless disabled); one GPU only."""
+
+import json
+import os
+import subprocess
+import sys
+
+import pytest
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+BENCH = os.path.join(REPO, "bench.py")
+
+
+def run_bench(*args, timeout=240):
+    return subprocess.run([sys.executable, BENCH, *args], cwd=REPO, capture_output=True, text=True,
+                          timeout=timeout)
+
+
+def test_bench_rejects_more_than_one_gpu():
+    proc = run_bench("--gpus", "2")
+    assert proc.returncode == 2
+    assert "one GPU only" in proc.stderr
+    assert proc.stdout.strip() == ""
+
+
+def test_algorithmic_bytes_closed_form():
+    """bytes = 4(M+1) + (4 + s)nnz + s N K_ref + s M N, K_ref = distinct
+    columns: a hand-counted 3x5 CSR, and configuration 1 against the
+    survey's figure of 17,891,332 bytes (which counts all 16384 columns;
+    the generated matrix leaves a few unused)."""
+    import numpy as np
+
+    import workloads as W
+
+    class Tiny:
+        rows, cols, nnz, dtype = 3, 5, 4, "fp16"
+        crow = np.array([0, 2, 2, 4])
+        col = np.array([1, 4, 1, 3])
+
+    # M=3: 16 bytes of rowptr; 4 nonzeros of 6 bytes; K_ref = 3 distinct
+    # columns {1, 3, 4} of 2*16 bytes each at N=16; output 3*16*2.
+    assert W.algorithmic_bytes(Tiny, 16) == 16 + 24 + 3 * 32 + 96
+    w = W.make(1)
+    unused = w.cols - np.unique(w.col).size
+    assert 0 <= unused < 32
+    assert W.algorithmic_bytes(w, 128) + 4 * 128 * unused == 17_891_332
+
+
+@pytest.mark.gpu
+def test_bench_json_line():
+    proc = run_bench("--steps", "3", "--warmup", "1", "--no-cpu", "--no-block-path", "--no-cold")
+    assert proc.returncode == 0, proc.stderr[-2000:]
+    lines = [line for line in proc.stdout.splitlines() if line.strip()]
+    assert len(lines) == 1
+    d = json.loads(lines[0])
+    for key in ("metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step", "higher_is_better",
+                "scaling", "vs_baseline", "dtype", "data", "config", "roofline"):
+        assert key in d, key
+    assert d["n_gpus"] == 1 and d["steps"] == 3 and d["warmup"] == 1
+    assert d["value"] > 0 and d["unit"] == "GFLOP/s" and d["dtype"] == "fp16"
+    assert "C2" in d["config"]["workload"]
+    r = d["roofline"]
+    for key in ("bound", "achieved", "peak", "unit", "frac", "traffic"):
+        assert key in r, key
+    assert r["bound"] == "hbm" and r["unit"] == "GB/s" and r["peak"] == 8000.0
+    assert abs(r["frac"] - r["achieved"] / r["peak"]) < 1e-3
+    assert r["traffic"] is None or r["traffic"] > 0
