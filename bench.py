@@ -56,6 +56,16 @@ MFMA_PEAK_TFLOPS = {"fp16": 2500.0, "fp32": 157.3}
 # traffic, Infinity Cache hits included.  Keyed by (config, op, width); the
 # runs are summarised in profiles/*_traffic.md.  Re-measured whenever the
 # kernels change.
+# The kernels one timed call launches (the roofline's event time covers all
+# of them, in launch order on one stream).
+OP_KERNELS = {
+    "csr": "gather_tiles + gather_post (one spmm_csr call)",
+    "mixed-empty": "gather_tiles + gather_post (spmm_ascend_cube, empty block part)",
+    "bcsr": "block_windows (+ block_combine when overflow ranges exist)",
+    "mixed": "gather_tiles + gather_post + block_windows (+ block_combine)",
+    "graph": ("fill_minus_one + scatter_inverse + gather_rows (pack) + gather_tiles + gather_post + "
+              "block_windows + block_combine + gather_rows (restore)"),
+}
 FETCH_SCALE = 2.0
 WRITE_SCALE = 1.0
 PMC_KIB = {
@@ -459,6 +469,7 @@ def main() -> int:
         "cold_cache_ms_per_call": None if cold_ms is None else round(cold_ms, 5),
         "roofline": {
             "bound": "hbm",
+            "kernels": OP_KERNELS.get(args.op, ""),
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
