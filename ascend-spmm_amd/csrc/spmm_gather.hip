@@ -28,9 +28,9 @@
 //    16 bytes per lane (the buffer range check returns zeros for the
 //    sentinel, so no position needs address arithmetic or a select), fp32
 //    FMAs, and a flush of the accumulated row at each row-end mark.
-//  * A short row (at most R/2 nonzeros) is summed entirely by the lane group
-//    of the range where it starts (running on into the next range, staged as
-//    a halo); the next range skips it.  So every such row is one
+//  * A short row (at most R/2 nonzeros, or R when R <= 32) is summed
+//    entirely by the lane group of the range where it starts (running on
+//    into the next range, staged as a halo); the next range skips it.  So every such row is one
 //    sequential fp32 sum, and only longer rows are split: they leave one fp32
 //    partial per range in the workspace ("tail" in the range where they
 //    start, "head" in every later range) and their id in the range's tail
@@ -70,10 +70,14 @@ constexpr int kStageUnroll = 18;
 #define SPMM_GATHER_SPLIT_BYTES 512
 #endif
 // A row is "short" (summed by one lane group, never split) when it holds at
-// most R / SPMM_GATHER_SHORT_DIV nonzeros.
-#ifndef SPMM_GATHER_SHORT_DIV
-#define SPMM_GATHER_SHORT_DIV 2
+// most short_max(R) nonzeros: R / 2, or all of R for ranges of at most
+// SPMM_GATHER_SHORT_FULL positions, where a lane group that runs on past its
+// range end adds little and the partials it avoids dominate (config 4's
+// vector part, R = 32).  A short row crosses at most one range end.
+#ifndef SPMM_GATHER_SHORT_FULL
+#define SPMM_GATHER_SHORT_FULL 32
 #endif
+inline int64_t short_max(int64_t range) { return range <= SPMM_GATHER_SHORT_FULL ? range : range / 2; }
 #ifndef SPMM_GATHER_TILE_RANGES
 #define SPMM_GATHER_TILE_RANGES 16
 #endif
@@ -93,6 +97,7 @@ struct Geometry {
   int64_t vrows;           // rowptr holds vrows + 1 entries; rows >= vrows are empty
   int64_t nnz;             // extent of col[] / value[]
   int64_t range;           // R, positions per range
+  int64_t short_max;       // longest "short" row: short_max(R)
   int64_t nranges;         // max(1, ceil(nnz / R))
   // Block part of the mixed operator (cwin == 0 for spmm_csr): the vector sum
   // of a row in a block window that has blocks goes to vpart in fp32 (the
@@ -432,7 +437,7 @@ __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM
   // its halo); each position is marked only by the row that holds it.  The
   // tile's rows run from rS while they start at or before P1 (the row holding
   // P1 included; later rows start in the next tile), below row_hi.  A short
-  // row (at most R / SPMM_GATHER_SHORT_DIV nonzeros) that crosses a range
+  // row (at most short_max(R) nonzeros) that crosses a range
   // boundary is owned by the range where it starts: s_cut tells that range
   // how far to run on and the next range where to begin.  A longer row leaves
   // one fp32 partial per range instead (s_long).  Empty rows are left to the
@@ -448,7 +453,7 @@ __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM
           sa.mark[b - 1 - P0] = static_cast<uint32_t>((r - rS + 1) << 1) | vp;
         }
         int64_t k = a < P0 ? 0 : (a - P0) / g.range + 1;  // first boundary after a
-        if (b - a <= g.range / SPMM_GATHER_SHORT_DIV) {
+        if (b - a <= g.short_max) {
           if (k <= nr && P0 + k * g.range < b) s_cut[k] = static_cast<int32_t>(b - P0);
         } else {
           for (; k <= nr && P0 + k * g.range < b; ++k) s_long[k] = r;
@@ -623,6 +628,7 @@ spmm_status gather_typed(const void* rowptr, const void* col, const void* value,
   g.vrows = vrows;
   g.nnz = nnz < 0 ? 0 : nnz;
   g.range = gather_range(g.nnz);
+  g.short_max = short_max(g.range);
   g.nranges = g.nnz > 0 ? ceil_div(g.nnz, g.range) : 1;
   g.Crowptr = static_cast<const I*>(Crowptr);
   g.cwin = Crowptr ? cwin : 0;
