@@ -163,6 +163,36 @@ __global__ void check_rowptr(const I* __restrict__ rowptr, int64_t nrows, int64_
   }
 }
 
+// The scalars the host needs after validation, gathered for one read-back:
+// rowptr[0], rowptr[rows] and the error bits.
+template <typename I>
+__global__ void collect_ends(const I* __restrict__ rowptr, int64_t rows, const int* __restrict__ err,
+                             int64_t* __restrict__ scal) {
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    scal[0] = static_cast<int64_t>(rowptr[0]);
+    scal[1] = static_cast<int64_t>(rowptr[rows]);
+    scal[2] = *err;
+  }
+}
+
+// The block count (last inclusive block id) and the error bits, for one read-back.
+__global__ void collect_blocks(const int64_t* __restrict__ bid, int64_t n, const int* __restrict__ err,
+                               int64_t* __restrict__ scal) {
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    scal[0] = n > 0 ? bid[n - 1] : 0;
+    scal[1] = *err;
+  }
+}
+
+// Two device scalars gathered for one read-back.
+__global__ void collect_pair(const int64_t* __restrict__ a, const int64_t* __restrict__ b,
+                             int64_t* __restrict__ scal) {
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    scal[0] = *a;
+    scal[1] = *b;
+  }
+}
+
 // Expands rows: for element e (position p = p_begin + e) records its row and
 // 64-bit column, checking column range and (optionally) ascending order.
 // Element-parallel, so a row of any length costs the same per element: each
@@ -498,6 +528,18 @@ struct TaskState {
   int64_t n_aic_blocks, vnnz;
   double est_aic, est_aiv, est_max;
 };
+
+// The AIC block count, the vector nonzero count and the error bits, read
+// back with the task state in two copies.
+__global__ void collect_taskmap(const TaskState* __restrict__ st, const int64_t* __restrict__ slot_ptr,
+                                const int64_t* __restrict__ vrow64, const int* __restrict__ err,
+                                int64_t* __restrict__ scal) {
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    scal[0] = slot_ptr[st->naic];
+    scal[1] = vrow64[st->out_rows];
+    scal[2] = *err;
+  }
+}
 
 __global__ void task_init(TaskState* __restrict__ s) {
   s->bpos = ~0ull;
@@ -872,6 +914,7 @@ constexpr int64_t kMagic = 0x5350'4d4d'5052'4531LL;
 struct WinSort {
   int64_t nmax = 0, nrows = 0, nwin = 0;
   int* err = nullptr;
+  int64_t* scal = nullptr;  // scalars read back to the host in one copy
   int64_t *row_of, *col64, *elem, *selem, *head, *bid, *blk_first, *blk_start, *blk_cnt,
       *elem_block, *win_start, *row_first;
   uint64_t *key, *skey, *blk_key;
@@ -882,6 +925,7 @@ struct WinSort {
     nmax = nnz;
     nwin = (rows + W - 1) / W;
     err = a.take<int>(4);
+    scal = a.take<int64_t>(4);
     row_of = a.take<int64_t>(nmax);
     col64 = a.take<int64_t>(nmax);
     key = a.take<uint64_t>(nmax);
@@ -945,16 +989,15 @@ spmm_status run_window_sort(const Csr& c, int64_t W, bool check_sorted, WinSort&
   if (c.rows > 0)
     launch(check_rowptr<I>, c.rows, s, static_cast<const I*>(c.rowptr), c.rows, c.nnz, S.err);
   if (spmm_status st = check_launch("check_rowptr")) return st;
-  I ends[2] = {0, 0};
-  int herr = 0;
-  if (spmm_status st = read_back(&ends[0], static_cast<const I*>(c.rowptr), 1, s)) return st;
-  if (spmm_status st = read_back(&ends[1], static_cast<const I*>(c.rowptr) + c.rows, 1, s)) return st;
-  if (spmm_status st = read_back(&herr, S.err, 1, s)) return st;
-  if (herr & kBadRowptr)
+  hipLaunchKernelGGL(collect_ends<I>, dim3(1), dim3(64), 0, s, static_cast<const I*>(c.rowptr), c.rows, S.err,
+                     S.scal);
+  int64_t v[3] = {0, 0, 0};
+  if (spmm_status st = read_back(v, S.scal, 3, s)) return st;
+  if (v[2] & kBadRowptr)
     return fail(SPMM_ERR_INVALID_ARGUMENT,
                 "invalid CSR row pointer: entries must be non-decreasing within [0, nnz]");
-  S.p_begin = static_cast<int64_t>(ends[0]);
-  S.n = static_cast<int64_t>(ends[1]) - S.p_begin;
+  S.p_begin = v[0];
+  S.n = v[1] - S.p_begin;
 
   if (c.rows > 0 && S.n > 0)
     launch(expand_rows<I>, (S.n + kExpandChunk - 1) / kExpandChunk * kT, s,
@@ -967,10 +1010,11 @@ spmm_status run_window_sort(const Csr& c, int64_t W, bool check_sorted, WinSort&
     return check_hip(e, "window sort");
   launch(run_heads, S.n, s, S.skey, S.n, S.head);
   if (hipError_t e = x.prims.inclusive_sum(S.head, S.bid, S.n)) return check_hip(e, "block scan");
-  S.nb = 0;
-  if (S.n > 0)
-    if (spmm_status st = read_back(&S.nb, S.bid + S.n - 1, 1, s)) return st;
-  if (spmm_status st = read_back(&herr, S.err, 1, s)) return st;
+  hipLaunchKernelGGL(collect_blocks, dim3(1), dim3(64), 0, s, S.bid, S.n, S.err, S.scal);
+  int64_t b[2] = {0, 0};
+  if (spmm_status st = read_back(b, S.scal, 2, s)) return st;
+  S.nb = b[0];
+  const int64_t herr = b[1];
   if (herr & kBadColumn) return fail(SPMM_ERR_CONTRACT, "column index out of range");
   if (herr & kUnsortedRow)
     return fail(SPMM_ERR_INVALID_ARGUMENT,
@@ -1139,8 +1183,12 @@ spmm_status hybrid_run(const Csr& c, double a, int64_t W, HybridArrays& H, Ctx& 
   launch(moved_elements, S.n + 1, s, S.elem_block, H.kept, S.n, H.eflag);
   if (hipError_t e = x.prims.exclusive_sum(H.eflag, H.vdst, S.n + 1)) return check_hip(e, "residual scan");
   if (spmm_status st = check_launch("hybrid split")) return st;
-  if (spmm_status st = read_back(kept_out, H.kscan + nb, 1, s)) return st;
-  return read_back(vnnz_out, H.vdst + S.n, 1, s);
+  hipLaunchKernelGGL(collect_pair, dim3(1), dim3(64), 0, s, H.kscan + nb, H.vdst + S.n, S.scal);
+  int64_t v[2] = {0, 0};
+  if (spmm_status st = read_back(v, S.scal, 2, s)) return st;
+  *kept_out = v[0];
+  *vnnz_out = v[1];
+  return SPMM_OK;
 }
 
 template <typename O>
@@ -1343,16 +1391,15 @@ spmm_status task_plan(const Csr& c, bool graph_layout, void* ws, size_t ws_bytes
   if (hipError_t e = x.prims.exclusive_sum(A.ocnt, A.vrow64, A.max_rows + 1)) return check_hip(e, "vrow scan");
   if (spmm_status st = check_launch("taskmapping")) return st;
 
+  hipLaunchKernelGGL(collect_taskmap, dim3(1), dim3(64), 0, s, A.st, A.slot_ptr, A.vrow64, S.err, S.scal);
   TaskState hs;
   if (spmm_status st = read_back(&hs, A.st, 1, s)) return st;
-  int herr = 0;
-  if (spmm_status st = read_back(&herr, S.err, 1, s)) return st;
-  if (herr & kBadOccupancy)
+  int64_t v[3] = {0, 0, 0};
+  if (spmm_status st = read_back(v, S.scal, 3, s)) return st;
+  if (v[2] & kBadOccupancy)
     return fail(SPMM_ERR_INVALID_ARGUMENT,
                 "block occupancy must be in [1, window_size]; coalesce duplicate CSR entries");
-  int64_t aic_blocks = 0, vnnz = 0;
-  if (spmm_status st = read_back(&aic_blocks, A.slot_ptr + hs.naic, 1, s)) return st;
-  if (spmm_status st = read_back(&vnnz, A.vrow64 + hs.out_rows, 1, s)) return st;
+  const int64_t aic_blocks = v[0], vnnz = v[1];
 
   spmm_taskmap_info r{};
   r.aic_windows = hs.naic;
