@@ -66,3 +66,19 @@ def test_bench_json_line():
     assert r["bound"] == "hbm" and r["unit"] == "GB/s" and r["peak"] == 8000.0
     assert abs(r["frac"] - r["achieved"] / r["peak"]) < 1e-3
     assert r["traffic"] is None or r["traffic"] > 0
+
+
+@pytest.mark.gpu
+def test_bench_preprocess_line():
+    """--op preprocess: the four GPU pipelines timed, the oracle's C port
+    beside them (kind "port"), one JSON line."""
+    proc = run_bench("--op", "preprocess", "--config", "1", "--steps", "2", "--warmup", "1")
+    assert proc.returncode == 0, proc.stderr[-2000:]
+    lines = [line for line in proc.stdout.splitlines() if line.strip()]
+    assert len(lines) == 1
+    d = json.loads(lines[0])
+    assert set(d["pipelines"]) == {"csr_to_bcsr", "csr_to_ascend_cube", "block_level_split", "preprocess"}
+    for p in d["pipelines"].values():
+        assert p["ms"] > 0 and p["bytes"] > 0 and p["cpu_ms"] > 0
+    assert d["cpu_baseline"]["kind"] == "port" and d["cpu_baseline"]["cores"] == 1
+    assert d["roofline"]["bound"] == "hbm" and d["value"] > 0
