@@ -30,11 +30,11 @@ __global__ __launch_bounds__(256) void gather_rows(const char* __restrict__ src,
     U* d = reinterpret_cast<U*>(dst) + r * units;
     if (s >= 0 && s < src_rows) {
       const U* sp = reinterpret_cast<const U*>(src) + s * units;
-      for (int64_t u = lane; u < units; u += 64) d[u] = sp[u];
+      for (int64_t u = lane; u < units; u += 64) __builtin_nontemporal_store(sp[u], d + u);
     } else {
       U z;
       __builtin_memset(&z, 0, sizeof(U));
-      for (int64_t u = lane; u < units; u += 64) d[u] = z;
+      for (int64_t u = lane; u < units; u += 64) __builtin_nontemporal_store(z, d + u);
     }
   }
 }

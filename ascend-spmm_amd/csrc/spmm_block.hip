@@ -229,9 +229,9 @@ __device__ inline void store_cols(T* p, const float* v) {
     half_c<C> h;
 #pragma unroll
     for (int i = 0; i < C; ++i) h[i] = static_cast<_Float16>(v[i]);
-    *reinterpret_cast<half_c<C>*>(p) = h;
+    __builtin_nontemporal_store(h, reinterpret_cast<half_c<C>*>(p));
   } else {
-    *reinterpret_cast<float4_t*>(p) = float4_t{v[0], v[1], v[2], v[3]};
+    __builtin_nontemporal_store(float4_t{v[0], v[1], v[2], v[3]}, reinterpret_cast<float4_t*>(p));
   }
 }
 
