@@ -69,9 +69,9 @@ OP_KERNELS = {
 FETCH_SCALE = 2.0
 WRITE_SCALE = 1.0
 PMC_KIB = {
-    (2, "csr", 128): {"fetch_kib": 205390.2 + 3879.9, "write_kib": 31384.8 + 659.8},
-    (3, "mixed", 128): {"fetch_kib": 51627.0 + 6313.1 + 131191.3 + 52.6,
-                        "write_kib": 12091.8 + 2266.5 + 14135.5 + 0.0},
+    (2, "csr", 128): {"fetch_kib": 203936.2 + 3879.9, "write_kib": 31384.0 + 659.8},
+    (3, "mixed", 128): {"fetch_kib": 51572.9 + 6313.1 + 130398.8 + 52.6,
+                        "write_kib": 12091.2 + 2266.5 + 14135.6 + 0.0},
 }
 
 def log(msg: str) -> None:
