@@ -69,9 +69,12 @@ OP_KERNELS = {
 FETCH_SCALE = 2.0
 WRITE_SCALE = 1.0
 PMC_KIB = {
-    (2, "csr", 128): {"fetch_kib": 203936.2 + 3879.9, "write_kib": 31384.0 + 659.8},
-    (3, "mixed", 128): {"fetch_kib": 51572.9 + 6313.1 + 130398.8 + 52.6,
-                        "write_kib": 12091.2 + 2266.5 + 14135.6 + 0.0},
+    (2, "csr", 128): {"fetch_kib": 203962.3 + 3879.9, "write_kib": 31384.1 + 659.8},
+    (3, "mixed", 128): {"fetch_kib": 51560.2 + 6313.1 + 130417.2 + 52.6,
+                        "write_kib": 12091.3 + 2266.5 + 14135.7 + 0.0},
+    (3, "bcsr", 128): {"fetch_kib": 47337.4 + 58.0, "write_kib": 16403.8 + 0.0},
+    (4, "mixed", 512): {"fetch_kib": 215823.9 + 5290.2 + 188080.1 + 30.0,
+                        "write_kib": 114565.9 + 2119.0 + 92312.1 + 0.0},
 }
 
 def log(msg: str) -> None:
