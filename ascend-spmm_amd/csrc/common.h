@@ -71,7 +71,21 @@ spmm_status launch_gather(int32_t index_type, int32_t value_type,
                           const void* dense, int64_t dense_rows, int64_t width,
                           void* out, void* workspace, size_t workspace_bytes,
                           const void* Crowptr, int64_t cwin, int64_t climit, float* vpart,
-                          hipStream_t stream);
+                          const void* Ccol, int32_t* order, hipStream_t stream);
+
+// Locality order of the block windows: with `order` set, one extra
+// work-group of the gather kernel, running beside the gathers, sorts the cwin
+// windows into kOrderBuckets buckets of their first block column (Ccol), and
+// the block kernel follows that order.  Used for at most kOrderMaxWindows
+// windows, dense rows of at least kOrderMinRowBytes, and a vector part (the
+// gather kernel runs).
+constexpr int64_t kOrderMaxWindows = 16384;
+constexpr int kOrderBuckets = 1024;
+constexpr int64_t kOrderMinRowBytes = 512;
+inline bool block_order_wanted(int64_t windows, int64_t vector_nnz, int64_t width, int32_t value_type) {
+  const int64_t row_bytes = width * (value_type == SPMM_VALUE_F16 ? 2 : 4);
+  return windows > 0 && windows <= kOrderMaxWindows && vector_nnz > 0 && row_bytes >= kOrderMinRowBytes;
+}
 
 // Thread-per-row scalar CSR baseline over rows [0, rows) (no workspace).
 spmm_status launch_rowscalar(int32_t index_type, int32_t value_type, const void* rowptr, const void* col,
@@ -108,6 +122,7 @@ spmm_status launch_block(int32_t index_type, int32_t value_type,
                          int64_t windows, int64_t block_count, int64_t block_values,
                          const void* Vrowptr, int64_t vector_rows, int64_t vector_nnz,
                          const void* dense, int64_t dense_rows, int64_t width,
-                         void* out, const float* vpart, float* slots, hipStream_t stream);
+                         void* out, const float* vpart, float* slots, const int32_t* order,
+                         hipStream_t stream);
 
 }  // namespace spmm

@@ -102,6 +102,7 @@ struct BlockArgs {
   int64_t kbig, noverflow, per_xcd;
   int64_t stage;           // blocks staged in LDS at a time (multiple of the K-step)
   int zero_empty;          // no vector part: windows without blocks write their rows as zeros
+  const int32_t* order;    // locality order of the windows (from the gather post pass), or null
 
   __device__ inline int64_t crp(int64_t s) const { return clampi(static_cast<int64_t>(Crowptr[s]), 0, limit); }
   __device__ inline int64_t vrp(int64_t r) const {
@@ -426,8 +427,9 @@ __global__ __launch_bounds__(64 * kMaxWaves) __attribute__((amdgpu_waves_per_eu(
   const int64_t n16 = 16 * a.N;
   if (g < lead) {
     const int64_t idx = g / kXcds;
-    const int64_t s = ((idx / kBlockXcdRun) * kXcds + g % kXcds) * kBlockXcdRun + idx % kBlockXcdRun;
+    int64_t s = ((idx / kBlockXcdRun) * kXcds + g % kXcds) * kBlockXcdRun + idx % kBlockXcdRun;
     if (s >= a.windows) return;  // uniform over the work-group
+    if (a.order != nullptr) s = a.order[s];
     const int64_t b0 = a.crp(s);
     int64_t b1 = a.crp(s + 1);
     if (b1 <= b0) {  // empty window: its rows are the vector pass's, or zeros
@@ -515,7 +517,8 @@ template <typename T, typename I>
 spmm_status block_typed(const void* Crowptr, const void* Ccol, const void* Cvalue, int64_t windows,
                         int64_t block_count, int64_t block_values, const void* Vrowptr,
                         int64_t vector_rows, int64_t vector_nnz, const void* dense, int64_t K,
-                        int64_t N, void* out, const float* vpart, float* slots, hipStream_t stream) {
+                        int64_t N, void* out, const float* vpart, float* slots, const int32_t* order,
+                        hipStream_t stream) {
   if (windows <= 0) return SPMM_OK;
   if (K > static_cast<int64_t>(kBadCol) - 1)
     return fail(SPMM_ERR_CONTRACT, "dense has too many rows for 32-bit column ids");
@@ -536,6 +539,7 @@ spmm_status block_typed(const void* Crowptr, const void* Ccol, const void* Cvalu
   a.vpart = vpart;
   a.slots = slots;
   a.zero_empty = vector_nnz == 0 ? 1 : 0;
+  a.order = order;
   a.kbig = block_chunk_for(sizeof(T) == 2 ? SPMM_VALUE_F16 : SPMM_VALUE_F32, a.limit);
   a.noverflow = block_overflow_ranges(a.limit, a.kbig);
   a.first_of = reinterpret_cast<int64_t*>(slots + a.noverflow * 2 * 16 * N);
@@ -579,11 +583,11 @@ spmm_status launch_block(int32_t index_type, int32_t value_type, const void* Cro
                          int64_t block_count, int64_t block_values, const void* Vrowptr,
                          int64_t vector_rows, int64_t vector_nnz, const void* dense,
                          int64_t dense_rows, int64_t width, void* out, const float* vpart,
-                         float* slots, hipStream_t stream) {
+                         float* slots, const int32_t* order, hipStream_t stream) {
 #define SPMM_BLOCK_CALL(T, I)                                                                   \
   return block_typed<T, I>(Crowptr, Ccol, Cvalue, windows, block_count, block_values, Vrowptr, \
                            vector_rows, vector_nnz, dense, dense_rows, width, out, vpart, slots, \
-                           stream)
+                           order, stream)
   if (value_type == SPMM_VALUE_F16) {
     if (index_type == SPMM_INDEX_I32) SPMM_BLOCK_CALL(_Float16, int32_t);
     SPMM_BLOCK_CALL(_Float16, int64_t);

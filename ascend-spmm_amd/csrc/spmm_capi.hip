@@ -99,7 +99,7 @@ spmm_status spmm_csr_run(const spmm_csr_desc* d, const void* rowptr, const void*
   if (spmm_status st = check_aligned(dense, out, "spmm_csr")) return st;
   return launch_gather(d->index_type, d->value_type, rowptr, col, value, d->nnz, d->rows, 0, d->rows,
                        dense, d->dense_rows, d->width, out, workspace, workspace_bytes, nullptr, 0, 0,
-                       nullptr, as_stream(stream));
+                       nullptr, nullptr, nullptr, as_stream(stream));
 }
 
 spmm_status spmm_csr_rowscalar_run(const spmm_csr_desc* d, const void* rowptr, const void* col,
@@ -134,7 +134,7 @@ namespace {
 // than the block chunk ([ranges][2][16][width]) and the window starting in
 // each overflow range ([ranges] int64).
 struct MixedLayout {
-  size_t gather = 0, vpart = 0, slots = 0;
+  size_t gather = 0, vpart = 0, slots = 0, order = 0;
   int64_t limit = 0;
   explicit MixedLayout(const spmm_mixed_desc* d) {
     const int64_t w = d->width > 0 ? d->width : 0;
@@ -148,8 +148,12 @@ struct MixedLayout {
     const int64_t ranges = block_overflow_ranges(limit, block_chunk_for(d->value_type, limit));
     slots = align_up(static_cast<size_t>(ranges * 2 * 16) * w * sizeof(float) +
                          static_cast<size_t>(ranges) * sizeof(int64_t), 256);
+    // The block windows' locality order (block_order_wanted).
+    order = block_order_wanted(d->block_windows, d->vector_nnz, w, d->value_type)
+                ? align_up(static_cast<size_t>(d->block_windows) * sizeof(int32_t), 256)
+                : 0;
   }
-  size_t total() const { return gather + vpart + slots; }
+  size_t total() const { return gather + vpart + slots + order; }
 };
 }  // namespace
 
@@ -191,19 +195,22 @@ spmm_status spmm_mixed_run(const spmm_mixed_desc* d, const void* Crowptr, const 
   char* ws = static_cast<char*>(workspace);
   float* vpart = lay.vpart > 0 ? reinterpret_cast<float*>(ws + lay.gather) : nullptr;
   float* slots = reinterpret_cast<float*>(ws + lay.gather + lay.vpart);
+  int32_t* order = lay.order > 0 ? reinterpret_cast<int32_t*>(ws + lay.gather + lay.vpart + lay.slots) : nullptr;
   // Vector pass first (it leaves the fp32 vector sums of block-window rows in
   // vpart), then the block part, which adds them and rounds once.  Without
   // vector nonzeros the block kernel writes the zero rows of windows without
   // blocks itself, and the vector pass only covers rows past the windows.
+  // With the window order (block_order_wanted), the vector pass's kernel also
+  // writes the block windows' locality order, which the block kernel follows.
   const int64_t row_lo = d->vector_nnz == 0 ? 16 * d->block_windows : 0;
   spmm_status st = launch_gather(d->index_type, d->value_type, Vrowptr, Vcol, Vvalue, d->vector_nnz,
                                  d->vector_rows, row_lo, out_rows, dense, d->dense_rows, d->width, out, ws,
                                  lay.gather, d->block_windows > 0 ? Crowptr : nullptr, d->block_windows,
-                                 lay.limit, vpart, s);
+                                 lay.limit, vpart, Ccol, order, s);
   if (st != SPMM_OK) return st;
   return launch_block(d->index_type, d->value_type, Crowptr, Ccol, Cvalue, d->block_windows,
                       d->block_count, d->block_values, Vrowptr, d->vector_rows, d->vector_nnz, dense,
-                      d->dense_rows, d->width, out, vpart, slots, s);
+                      d->dense_rows, d->width, out, vpart, slots, order, s);
 }
 
 }  // extern "C"

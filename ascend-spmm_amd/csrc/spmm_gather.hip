@@ -106,6 +106,11 @@ struct Geometry {
   const I* Crowptr;
   int64_t cwin, climit;
   float* vpart;
+  // Locality order of the block windows, written by the gather kernel's extra
+  // work-group when set.
+  const I* Ccol;
+  int64_t K;
+  int32_t* order;
 
   __device__ inline int64_t rp(int64_t r) const {
     return clampi(static_cast<int64_t>(rowptr[r < vrows ? r : vrows]), 0, nnz);
@@ -358,6 +363,97 @@ __device__ inline int64_t find_row(const Geometry<I>& g, int64_t P) {
   return lo;
 }
 
+// Locality order of the cwin block windows (one work-group of any size from
+// 32 threads, LDS: kOrderBuckets + 1024 int32): a counting sort by the
+// window's first block column in kOrderBuckets buckets over [0, K).  Windows
+// that gather the same dense rows end up next to each other, and the block
+// kernel deals consecutive positions of the order to one XCD.  Any
+// permutation gives the same results (every window is summed by its own
+// work-group), so ties within a bucket take the order of the LDS atomics.
+//
+// The order only pays where windows are local (their block columns span a
+// small part of [0, K), as in banded or clustered matrices).  When fewer than
+// half the windows span less than K / kOrderLocalDiv columns, the identity
+// order is written instead.
+constexpr int64_t kOrderLocalDiv = 8;
+
+template <typename I>
+__device__ void order_windows(const Geometry<I>& g, int32_t* cnt, int32_t* part) {
+  const int tid = threadIdx.x, nt = blockDim.x;
+  __shared__ int32_t s_local;
+  auto bucket = [&](int64_t b0, int64_t b1, int64_t c) -> int {
+    if (b1 <= b0 || g.K <= 0) return 0;
+    return static_cast<int>(clampi(c, 0, g.K - 1) * kOrderBuckets / g.K);
+  };
+  for (int i = tid; i < kOrderBuckets; i += nt) cnt[i] = 0;
+  if (tid == 0) s_local = 0;
+  __syncthreads();
+  constexpr int kU = 4;  // windows per thread per round, their loads issued together
+  for (int pass = 0; pass < 2; ++pass) {  // 0: histogram; 1: scatter (keys recomputed)
+    int32_t local = 0;
+    for (int64_t s0 = 0; s0 < g.cwin; s0 += int64_t(nt) * kU) {
+      int64_t b0[kU], b1[kU], c[kU], e[kU];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const int64_t s = s0 + int64_t(u) * nt + tid;
+        b0[u] = s < g.cwin ? g.crp(s) : 0;
+        b1[u] = s < g.cwin ? g.crp(s + 1) : 0;
+      }
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        c[u] = b1[u] > b0[u] ? static_cast<int64_t>(g.Ccol[b0[u]]) : 0;
+        e[u] = pass == 0 && b1[u] > b0[u] ? static_cast<int64_t>(g.Ccol[b1[u] - 1]) : 0;
+      }
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const int64_t s = s0 + int64_t(u) * nt + tid;
+        if (s >= g.cwin) continue;
+        const int k = bucket(b0[u], b1[u], c[u]);
+        if (pass == 0) {
+          atomicAdd(&cnt[k], 1);
+          const int64_t span = e[u] > c[u] ? e[u] - c[u] : c[u] - e[u];
+          local += span * kOrderLocalDiv < g.K ? 1 : 0;
+        } else {
+          g.order[atomicAdd(&cnt[k], 1)] = static_cast<int32_t>(s);
+        }
+      }
+    }
+    if (pass == 1) break;
+    atomicAdd(&s_local, local);
+    __syncthreads();
+    if (2 * static_cast<int64_t>(s_local) < g.cwin) {  // not local: identity order
+      for (int64_t s = tid; s < g.cwin; s += nt) g.order[s] = static_cast<int32_t>(s);
+      return;
+    }
+    // Exclusive scan of the bucket counts: per-thread runs, then a
+    // Hillis-Steele scan of the run sums (nt <= 1024).
+    const int per = (kOrderBuckets + nt - 1) / nt;
+    int32_t sum = 0;
+    for (int k = 0; k < per; ++k) {
+      const int i = tid * per + k;
+      if (i < kOrderBuckets) sum += cnt[i];
+    }
+    part[tid] = sum;
+    __syncthreads();
+    for (int off = 1; off < nt; off *= 2) {
+      const int32_t t = tid >= off ? part[tid - off] : 0;
+      __syncthreads();
+      part[tid] += t;
+      __syncthreads();
+    }
+    int32_t run = part[tid] - sum;
+    for (int k = 0; k < per; ++k) {
+      const int i = tid * per + k;
+      if (i < kOrderBuckets) {
+        const int32_t v = cnt[i];
+        cnt[i] = run;
+        run += v;
+      }
+    }
+    __syncthreads();
+  }
+}
+
 #ifndef SPMM_GATHER_WAVES
 #define SPMM_GATHER_WAVES 5
 #endif
@@ -384,9 +480,22 @@ __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM
   // part g % kXcds % wg_split of a contiguous run of tiles, so neighbouring
   // tiles, whose rows tend to share dense rows, share an L2, and with
   // wg_split > 1 each XCD's L2 serves one column chunk of the dense rows.
-  const int64_t xcd = static_cast<int64_t>(blockIdx.x) % kXcds;
+  // With a window order to write, work-groups [0, kXcds) come first: the
+  // first one sorts the windows while the gathers run, the others exit.
+  int64_t bid = static_cast<int64_t>(blockIdx.x);
+  if (g.order != nullptr) {
+    if (bid < kXcds) {
+      if (bid == 0) {
+        int32_t* ord = reinterpret_cast<int32_t*>(smem);
+        order_windows(g, ord, ord + kOrderBuckets);
+      }
+      return;
+    }
+    bid -= kXcds;
+  }
+  const int64_t xcd = bid % kXcds;
   const int64_t part = xcd % wg_split;
-  const int64_t idx = static_cast<int64_t>(blockIdx.x) / kXcds;
+  const int64_t idx = bid / kXcds;
   const int64_t tile = ((idx / kXcdRun) * (kXcds / wg_split) + xcd / wg_split) * kXcdRun + idx % kXcdRun;
   if (tile >= tiles) return;  // uniform over the work-group, before any barrier
   const int64_t j0 = tile * ranges_per_tile;
@@ -618,7 +727,8 @@ template <typename T, typename I>
 spmm_status gather_typed(const void* rowptr, const void* col, const void* value, int64_t nnz,
                          int64_t vrows, int64_t row_lo, int64_t row_hi, const void* dense, int64_t K,
                          int64_t N, void* out, void* ws, size_t ws_bytes, const void* Crowptr,
-                         int64_t cwin, int64_t climit, float* vpart, hipStream_t stream) {
+                         int64_t cwin, int64_t climit, float* vpart, const void* Ccol, int32_t* order,
+                         hipStream_t stream) {
   constexpr int V = LaneVec<T>::V;
   if (row_hi <= row_lo) return SPMM_OK;
   Geometry<I> g;
@@ -634,6 +744,9 @@ spmm_status gather_typed(const void* rowptr, const void* col, const void* value,
   g.cwin = Crowptr ? cwin : 0;
   g.climit = climit;
   g.vpart = vpart;
+  g.Ccol = static_cast<const I*>(Ccol);
+  g.K = K;
+  g.order = Crowptr && cwin > 0 && cwin <= kOrderMaxWindows && nnz > 0 ? order : nullptr;
 
   if (K > static_cast<int64_t>(kBadCol) - 1)
     return fail(SPMM_ERR_CONTRACT, "dense has too many rows for 32-bit column ids");
@@ -673,7 +786,8 @@ spmm_status gather_typed(const void* rowptr, const void* col, const void* value,
 
   if (g.nnz > 0) {
     const int64_t tiles = ceil_div(g.nranges, ranges_per_tile);
-    const size_t lds = static_cast<size_t>((ranges_per_tile + 1) * g.range) * Staged<T>::bytes_per_position();
+    size_t lds = static_cast<size_t>((ranges_per_tile + 1) * g.range) * Staged<T>::bytes_per_position();
+    if (g.order && lds < (kOrderBuckets + 1024) * sizeof(int32_t)) lds = (kOrderBuckets + 1024) * sizeof(int32_t);
     // Dense operands within a 32-bit byte extent use buffer loads.
     const bool buffer = K * N * static_cast<int64_t>(sizeof(T)) <= kBufferLimit;
     auto kernel = buffer ? gather_tiles<T, I, BufferLoader<T>> : gather_tiles<T, I, GlobalLoader<T>>;
@@ -681,7 +795,7 @@ spmm_status gather_typed(const void* rowptr, const void* col, const void* value,
     if (kXcds % wg_split != 0) return fail(SPMM_ERR_CONTRACT, "gather: column split does not divide the XCDs");
     const int64_t groups = kXcds / wg_split;
     const int64_t tiles_per_group = ceil_div(tiles, groups * kXcdRun) * kXcdRun;
-    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(kXcds * tiles_per_group)),
+    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(kXcds * tiles_per_group + (g.order ? kXcds : 0))),
                        dim3(static_cast<unsigned>(wg_threads)), lds, stream, g,
                        static_cast<const I*>(col), static_cast<const T*>(value),
                        static_cast<const T*>(dense), K, N, static_cast<T*>(out), partial, log2L,
@@ -710,11 +824,11 @@ spmm_status launch_gather(int32_t index_type, int32_t value_type, const void* ro
                           int64_t row_lo, int64_t row_hi, const void* dense, int64_t dense_rows,
                           int64_t width, void* out, void* workspace, size_t workspace_bytes,
                           const void* Crowptr, int64_t cwin, int64_t climit, float* vpart,
-                          hipStream_t stream) {
+                          const void* Ccol, int32_t* order, hipStream_t stream) {
 #define SPMM_GATHER_CALL(T, I)                                                                 \
   return gather_typed<T, I>(rowptr, col, value, nnz, vrows, row_lo, row_hi, dense, dense_rows, \
                             width, out, workspace, workspace_bytes, Crowptr, cwin, climit, vpart, \
-                            stream)
+                            Ccol, order, stream)
   if (value_type == SPMM_VALUE_F16) {
     if (index_type == SPMM_INDEX_I32) SPMM_GATHER_CALL(_Float16, int32_t);
     SPMM_GATHER_CALL(_Float16, int64_t);

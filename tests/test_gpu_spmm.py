@@ -172,6 +172,44 @@ def test_block_path_width_invariant_bitwise(spmm_npu, dtype):
         assert torch.equal(part, full[:, :n]), f"width {n} differs"
 
 
+def test_block_window_order_on_a_banded_layout(spmm_npu):
+    """The preprocess layout of a banded matrix (windows sorted by density,
+    each spanning a narrow band of columns) at N >= 256 fp16 takes the block
+    windows' locality order.  The order changes only which work-group runs
+    first, so the result equals the N=128 run (no order) bit for bit on its
+    columns, and the restored rows match A @ B."""
+    rng = np.random.default_rng(97)
+    rows, band = 3000, 48
+    deg = rng.integers(0, 2 * band, rows)
+    deg[rng.random(rows) < 0.2] = 2  # some sparse rows, for the vector part
+    parts = []
+    for r in range(rows):
+        lo, hi = max(0, r - band), min(rows, r + band)
+        parts.append(np.sort(rng.choice(np.arange(lo, hi), min(int(deg[r]), hi - lo), replace=False)))
+    crow = np.zeros(rows + 1, np.int64)
+    crow[1:] = np.cumsum([p.size for p in parts])
+    col = np.concatenate(parts).astype(np.int64)
+    vals = rng.uniform(-1, 1, col.size).astype(np.float16)
+    B = rng.standard_normal((rows, 512)).astype(np.float16)
+    p = spmm_npu.preprocess(torch.from_numpy(crow), torch.from_numpy(col), torch.from_numpy(vals), rows, rows, 16)
+    assert p["unique_col_ids"].numel() > 0 and p["vcol_indices"].numel() > 0
+    i32 = torch.int32
+
+    def run(Bn):
+        return spmm_npu.spmm_ascend_cube(
+            p["crow_window_ptr"].to("cuda", i32), p["unique_col_ids"].to("cuda", i32), p["value"].cuda(),
+            p["vrow_window_ptr"].to("cuda", i32), p["vcol_indices"].to("cuda", i32), p["vvalue"].cuda(),
+            dev(Bn), dev(O.make_start(p["crow_window_ptr"].numpy(), 20)),
+            dev(O.make_start(p["vrow_window_ptr"].numpy(), 40)))
+
+    base = run(np.ascontiguousarray(B[:, :128])).cpu()
+    for n in (256, 512):
+        out = run(np.ascontiguousarray(B[:, :n]))
+        assert torch.equal(out[:, :128].cpu(), base), f"width {n} differs from 128"
+        got = spmm_npu.restore_node_tensor(out, p["inv_permutation"].cuda())[:rows]
+        assert_close(got, O.spmm_f64(crow, col, vals, B[:, :n]), "fp16")
+
+
 @pytest.mark.parametrize("dtype", ["fp16", "fp32"])
 @pytest.mark.parametrize("width", [16, 128, 256])
 def test_mixed_with_empty_block_part_equals_csr_bitwise(spmm_npu, dtype, width):
