@@ -458,7 +458,7 @@ __device__ void order_windows(const Geometry<I>& g, int32_t* cnt, int32_t* part)
 #define SPMM_GATHER_WAVES 5
 #endif
 // Waves per SIMD the register budget of gather_tiles is fitted to.
-template <typename T, typename I, typename Loader>
+template <typename T, typename I, typename Loader, bool kOrder>
 __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM_GATHER_WAVES))) void gather_tiles(
     Geometry<I> g, const I* __restrict__ col, const T* __restrict__ value,
     const T* __restrict__ dense, int64_t K, int64_t N, T* __restrict__ out, float* __restrict__ ws,
@@ -480,10 +480,12 @@ __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM
   // part g % kXcds % wg_split of a contiguous run of tiles, so neighbouring
   // tiles, whose rows tend to share dense rows, share an L2, and with
   // wg_split > 1 each XCD's L2 serves one column chunk of the dense rows.
-  // With a window order to write, work-groups [0, kXcds) come first: the
-  // first one sorts the windows while the gathers run, the others exit.
+  // With a window order to write (kOrder: a separate instantiation, so the
+  // plain gather keeps its register budget), work-groups [0, kXcds) come
+  // first: the first one sorts the windows while the gathers run, the others
+  // exit.
   int64_t bid = static_cast<int64_t>(blockIdx.x);
-  if (g.order != nullptr) {
+  if constexpr (kOrder) {
     if (bid < kXcds) {
       if (bid == 0) {
         int32_t* ord = reinterpret_cast<int32_t*>(smem);
@@ -790,7 +792,8 @@ spmm_status gather_typed(const void* rowptr, const void* col, const void* value,
     if (g.order && lds < (kOrderBuckets + 1024) * sizeof(int32_t)) lds = (kOrderBuckets + 1024) * sizeof(int32_t);
     // Dense operands within a 32-bit byte extent use buffer loads.
     const bool buffer = K * N * static_cast<int64_t>(sizeof(T)) <= kBufferLimit;
-    auto kernel = buffer ? gather_tiles<T, I, BufferLoader<T>> : gather_tiles<T, I, GlobalLoader<T>>;
+    auto kernel = g.order ? (buffer ? gather_tiles<T, I, BufferLoader<T>, true> : gather_tiles<T, I, GlobalLoader<T>, true>)
+                          : (buffer ? gather_tiles<T, I, BufferLoader<T>, false> : gather_tiles<T, I, GlobalLoader<T>, false>);
     // kXcds / wg_split groups of XCDs take runs of kXcdRun tiles in turn.
     if (kXcds % wg_split != 0) return fail(SPMM_ERR_CONTRACT, "gather: column split does not divide the XCDs");
     const int64_t groups = kXcds / wg_split;
