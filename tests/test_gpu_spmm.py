@@ -172,12 +172,14 @@ def test_block_path_width_invariant_bitwise(spmm_npu, dtype):
         assert torch.equal(part, full[:, :n]), f"width {n} differs"
 
 
-def test_block_window_order_on_a_banded_layout(spmm_npu):
+@pytest.mark.parametrize("dtype", ["fp16", "fp32"])
+def test_block_window_order_on_a_banded_layout(spmm_npu, dtype):
     """The preprocess layout of a banded matrix (windows sorted by density,
-    each spanning a narrow band of columns) at N >= 256 fp16 takes the block
-    windows' locality order.  The order changes only which work-group runs
-    first, so the result equals the N=128 run (no order) bit for bit on its
-    columns, and the restored rows match A @ B."""
+    each spanning a narrow band of columns) with dense rows of 512 bytes or
+    more takes the block windows' locality order.  The order changes only
+    which work-group runs first, so the result equals a narrower run without
+    the order (fp16 N=128, fp32 N=64) bit for bit on its columns, and the
+    restored rows match A @ B."""
     rng = np.random.default_rng(97)
     rows, band = 3000, 48
     deg = rng.integers(0, 2 * band, rows)
@@ -189,8 +191,8 @@ def test_block_window_order_on_a_banded_layout(spmm_npu):
     crow = np.zeros(rows + 1, np.int64)
     crow[1:] = np.cumsum([p.size for p in parts])
     col = np.concatenate(parts).astype(np.int64)
-    vals = rng.uniform(-1, 1, col.size).astype(np.float16)
-    B = rng.standard_normal((rows, 512)).astype(np.float16)
+    vals = rng.uniform(-1, 1, col.size).astype(NP_DT[dtype])
+    B = rng.standard_normal((rows, 512)).astype(NP_DT[dtype])
     p = spmm_npu.preprocess(torch.from_numpy(crow), torch.from_numpy(col), torch.from_numpy(vals), rows, rows, 16)
     assert p["unique_col_ids"].numel() > 0 and p["vcol_indices"].numel() > 0
     i32 = torch.int32
@@ -202,12 +204,13 @@ def test_block_window_order_on_a_banded_layout(spmm_npu):
             dev(Bn), dev(O.make_start(p["crow_window_ptr"].numpy(), 20)),
             dev(O.make_start(p["vrow_window_ptr"].numpy(), 40)))
 
-    base = run(np.ascontiguousarray(B[:, :128])).cpu()
+    narrow = 128 if dtype == "fp16" else 64  # dense rows under 512 bytes: no order
+    base = run(np.ascontiguousarray(B[:, :narrow])).cpu()
     for n in (256, 512):
         out = run(np.ascontiguousarray(B[:, :n]))
-        assert torch.equal(out[:, :128].cpu(), base), f"width {n} differs from 128"
+        assert torch.equal(out[:, :narrow].cpu(), base), f"width {n} differs from {narrow}"
         got = spmm_npu.restore_node_tensor(out, p["inv_permutation"].cuda())[:rows]
-        assert_close(got, O.spmm_f64(crow, col, vals, B[:, :n]), "fp16")
+        assert_close(got, O.spmm_f64(crow, col, vals, B[:, :n]), dtype)
 
 
 @pytest.mark.parametrize("dtype", ["fp16", "fp32"])
