@@ -1,0 +1,183 @@
+"""Seeded medium-scale GPU parity sweep: matrices of a few thousand to tens
+of thousands of rows (several gather ranges per long row, many tiles, block
+windows with overflow chunks, window orders), drawn from five structure
+families, each checked through every operator path against the oracle:
+
+* spmm_csr against the fp64 product (the reference's tolerance,
+  tests/task_mapping/correctness.py:140-143) and bitwise against a
+  narrower run on the shared columns (the vector path's width invariance,
+  tests/aic_aiv_ablation/bitwise_correctness.py:138-175);
+* csr_to_bcsr, block_level_split and preprocess (graph layout on and off)
+  bit for bit against the oracle's layouts;
+* spmm_ascend_cube on each of those layouts against the fp64 product,
+  after restore_node_tensor where rows are packed.
+
+The bound is the reference's atol = rtol (2e-2 fp16, 1e-4 fp32) plus the
+rounding that fp32 accumulation of a row's d products p_k admits in any
+order: 4 u sqrt(d) sqrt(sum p_k^2), u = 2^-24 (about ten standard
+deviations of recursive summation's error, whose size is u n sigma for n
+terms of rms sigma).  It matters only for the hub rows of tens of thousands
+of nonzeros, where no fp32 summation order stays inside 1e-4 (a sequential
+fp32 sum of those rows misses it too); for rows of ordinary degree it is a
+small fraction of the reference's tolerance.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from test_gpu_preprocess import assert_same
+
+pytestmark = pytest.mark.gpu
+
+TOL = {np.float16: 2e-2, np.float32: 1e-4}
+FAMILIES = ("powerlaw", "banded", "mixed", "community", "hubs")
+
+
+def dev(a, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    return t if dtype is None else t.to(dtype)
+
+
+def close(out, expected, npdt, slack):
+    tol = TOL[npdt]
+    a = out.float().cpu().double().numpy()
+    bad = np.abs(a - expected) > tol + tol * np.abs(expected) + slack
+    assert not bad.any(), f"{int(bad.sum())} mismatches, max abs err {float(np.abs(a - expected).max()):.3e}"
+
+
+def accumulation_slack(crow, col, vals, B):
+    """4 u sqrt(d_r) sqrt(sum_k (a_rk B_kj)^2) per output element, u = 2^-24."""
+    v = vals.astype(np.float64)
+    d = np.diff(crow).astype(np.float64)[:, None]
+    s2 = O.spmm_f64(crow, col, v * v, B.astype(np.float64) ** 2)
+    return 4.0 * 2.0 ** -24 * np.sqrt(d) * np.sqrt(s2)
+
+
+def from_pairs(rows, cols, r, c):
+    """CSR with distinct sorted columns per row from (row, column) pairs
+    (duplicates dropped)."""
+    key = np.unique(r.astype(np.int64) * cols + c.astype(np.int64))
+    r, c = key // cols, key % cols
+    crow = np.zeros(rows + 1, np.int64)
+    np.add.at(crow, r + 1, 1)
+    return np.cumsum(crow), c.astype(np.int64)
+
+
+def matrix(family, rng):
+    """One square matrix of the family; sizes are drawn per case."""
+    n = int(rng.integers(2000, 60000))
+    if family == "powerlaw":  # Zipf degrees, uniform columns (configuration 2's shape)
+        deg = np.minimum(rng.zipf(float(rng.uniform(1.5, 2.2)), n), min(n, 3000))
+        deg[rng.random(n) < 0.1] = 0
+        r = np.repeat(np.arange(n), deg)
+        c = rng.integers(0, n, r.size)
+    elif family == "banded":  # 16x16 blocks on a band of block diagonals (configuration 3's shape)
+        nb, band = (n + 15) // 16, int(rng.integers(1, 9))
+        bi = np.repeat(np.arange(nb), 2 * band + 1)
+        bj = bi + np.tile(np.arange(-band, band + 1), nb)
+        keep = (bj >= 0) & (bj < nb) & (rng.random(bi.size) < 0.6)
+        bi, bj = bi[keep], bj[keep]
+        fill = rng.random((bi.size, 16, 16)) < float(rng.uniform(0.3, 0.9))
+        k, y, x = np.nonzero(fill)
+        r, c = bi[k] * 16 + y, bj[k] * 16 + x
+        keep = (r < n) & (c < n)
+        r, c = r[keep], c[keep]
+    elif family == "mixed":  # block windows interleaved with sparse windows (configuration 4's shape)
+        nw = (n + 15) // 16
+        blocky = rng.random(nw) < 0.5
+        rs, cs = [], []
+        for w in np.nonzero(blocky)[0]:
+            for bj in rng.integers(0, (n + 15) // 16, 4):
+                y, x = np.nonzero(rng.random((16, 16)) < 0.5)
+                rs.append(w * 16 + y)
+                cs.append(bj * 16 + x)
+        sparse_rows = np.nonzero(~blocky[np.arange(n) // 16])[0]
+        rs.append(np.repeat(sparse_rows, 4))
+        cs.append(rng.integers(0, n, sparse_rows.size * 4))
+        r, c = np.concatenate(rs), np.concatenate(cs)
+        keep = (r < n) & (c < n)
+        r, c = r[keep], c[keep]
+    elif family == "community":  # most columns within the row's community (configuration 5's shape)
+        size = int(rng.integers(64, 2048))
+        deg = np.minimum(rng.zipf(2.0, n), 2000)
+        r = np.repeat(np.arange(n), deg)
+        local = rng.random(r.size) < 0.7
+        base = (r // size) * size
+        c = np.where(local, base + rng.integers(0, size, r.size), rng.integers(0, n, r.size))
+        c = np.minimum(c, n - 1)
+    else:  # "hubs": a few rows holding most columns, long runs of empty rows
+        deg = rng.integers(0, 6, n)
+        deg[rng.random(n) < 0.5] = 0
+        deg[rng.integers(0, n, 4)] = n
+        r = np.repeat(np.arange(n), deg)
+        c = rng.integers(0, n, r.size)
+    crow, col = from_pairs(n, n, r, c)
+    return n, crow, col
+
+
+CASES = [(f, s) for s in range(8) for f in FAMILIES]
+
+
+@pytest.mark.parametrize("family,seed", CASES, ids=[f"{f}-{s}" for f, s in CASES])
+def test_sweep(spmm_npu, family, seed):
+    rng = np.random.default_rng(1000 * seed + FAMILIES.index(family))
+    n, crow, col = matrix(family, rng)
+    half = bool((seed + FAMILIES.index(family)) % 2)
+    npdt = np.float16 if half else np.float32
+    vals = rng.uniform(-1, 1, col.size).astype(npdt)
+    widths = [16, 64, 128, 256, 512] + ([1024] if half else [])
+    N = int(rng.choice(widths[1:]))
+    B = rng.standard_normal((n, N)).astype(npdt)
+    expected = O.spmm_f64(crow, col, vals, B)
+    slack = accumulation_slack(crow, col, vals, B)
+    print(f"[sweep] {family} seed={seed} rows={n} nnz={col.size} N={N} {npdt.__name__}", flush=True)
+
+    # spmm_csr: tolerance, then width invariance on the first 16 columns.
+    it = torch.int64 if seed % 2 else torch.int32
+    start = dev(O.make_start(crow, 40))
+    out = spmm_npu.spmm_csr(dev(crow, it), dev(col, it), dev(vals), dev(B), start)
+    close(out, expected, npdt, slack)
+    narrow = spmm_npu.spmm_csr(dev(crow, it), dev(col, it), dev(vals), dev(np.ascontiguousarray(B[:, :16])), start)
+    assert torch.equal(out[:, :16].cpu(), narrow.cpu()), "vector path differs across widths"
+
+    i32 = torch.int32
+    empty_i = torch.zeros(0, dtype=i32, device="cuda")
+    empty_v = torch.zeros(0, dtype=dev(vals).dtype, device="cuda")
+
+    # csr_to_bcsr: bit-exact layout, then the pure block part.
+    b = O.csr_to_bcsr(crow, col, vals, n, n, 16)
+    assert_same(spmm_npu.csr_to_bcsr(dev(crow), dev(col), dev(vals), n, n, 16), b)
+    out = spmm_npu.spmm_ascend_cube(dev(b["crow_window_ptr"], i32), dev(b["unique_col_ids"], i32), dev(b["value"]),
+                                    torch.zeros(1, dtype=i32, device="cuda"), empty_i, empty_v, dev(B),
+                                    dev(O.make_start(b["crow_window_ptr"], 20)),
+                                    torch.zeros(40, dtype=i32, device="cuda"))
+    close(out[:n], expected, npdt, slack)
+
+    # block_level_split: bit-exact layout, then the mixed op.
+    a = float(rng.choice([(222.0 / 190.0) * 0.5, 295.0 / 505.0, 0.1, 3.0]))
+    h = O.block_level_split(crow, col, vals, n, n, a, 16)
+    assert_same(spmm_npu.block_level_split(torch.from_numpy(crow), torch.from_numpy(col), torch.from_numpy(vals),
+                                           n, n, a, 16), h)
+    out = spmm_npu.spmm_ascend_cube(
+        dev(h["crow_window_ptr"], i32), dev(h["unique_col_ids"], i32), dev(h["value"]),
+        dev(h["vrow_window_ptr"], i32), dev(h["vcol_indices"], i32), dev(h["vvalue"]), dev(B),
+        dev(O.make_start(h["crow_window_ptr"], 20)), dev(O.make_start(h["vrow_window_ptr"], 40)))
+    close(out[:n], expected, npdt, slack)
+
+    # preprocess, both layouts: bit-exact, then the mixed op on packed rows.
+    for graph_layout in (False, True):
+        p = O.preprocess(crow, col, vals, n, n, 16, graph_layout)
+        assert_same(spmm_npu.preprocess(dev(crow), dev(col), dev(vals), n, n, 16, graph_layout), p)
+        ccol = p["renumbered_unique_col_ids"] if graph_layout else p["unique_col_ids"]
+        vcol = p["renumbered_vcol_indices"] if graph_layout else p["vcol_indices"]
+        inv = torch.from_numpy(p["inv_permutation"])
+        dense = dev(B)
+        if graph_layout:
+            dense = spmm_npu.pack_node_tensor(dense, inv, int(p["packed_rows"][0]))
+        out = spmm_npu.spmm_ascend_cube(
+            dev(p["crow_window_ptr"], i32), dev(ccol, i32), dev(p["value"]),
+            dev(p["vrow_window_ptr"], i32), dev(vcol, i32), dev(p["vvalue"]), dense,
+            dev(O.make_start(p["crow_window_ptr"], 20)), dev(O.make_start(p["vrow_window_ptr"], 40)))
+        close(spmm_npu.restore_node_tensor(out, inv), expected, npdt, slack)
