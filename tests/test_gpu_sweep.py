@@ -1,14 +1,15 @@
 """Seeded medium-scale GPU parity sweep: matrices of a few thousand to tens
 of thousands of rows (several gather ranges per long row, many tiles, block
-windows with overflow chunks, window orders), drawn from five structure
-families, each checked through every operator path against the oracle:
+windows with overflow chunks, window orders), drawn from six structure
+families (one rectangular), each checked through every operator path against the oracle:
 
 * spmm_csr against the fp64 product (the reference's tolerance,
   tests/task_mapping/correctness.py:140-143) and bitwise against a
   narrower run on the shared columns (the vector path's width invariance,
   tests/aic_aiv_ablation/bitwise_correctness.py:138-175);
-* csr_to_bcsr, block_level_split and preprocess (graph layout on and off)
-  bit for bit against the oracle's layouts;
+* csr_to_bcsr, block_level_split and preprocess (graph layout on and off,
+  on for square matrices only) bit for bit against the oracle's layouts,
+  with int32 indices on even seeds and int64 on odd;
 * spmm_ascend_cube on each of those layouts against the fp64 product,
   after restore_node_tensor where rows are packed.
 
@@ -32,7 +33,7 @@ from test_gpu_preprocess import assert_same
 pytestmark = pytest.mark.gpu
 
 TOL = {np.float16: 2e-2, np.float32: 1e-4}
-FAMILIES = ("powerlaw", "banded", "mixed", "community", "hubs")
+FAMILIES = ("powerlaw", "banded", "mixed", "community", "hubs", "rect")
 
 
 def dev(a, dtype=None):
@@ -66,8 +67,15 @@ def from_pairs(rows, cols, r, c):
 
 
 def matrix(family, rng):
-    """One square matrix of the family; sizes are drawn per case."""
+    """One matrix of the family (square but for "rect"); sizes are drawn
+    per case.  Returns rows, cols, crow, col."""
     n = int(rng.integers(2000, 60000))
+    if family == "rect":  # power-law rows over a column space 1/16 to 4 times the row count
+        cols = max(1, int(n * 2.0 ** rng.uniform(-4, 2)))
+        deg = np.minimum(rng.zipf(1.8, n), min(cols, 3000))
+        r = np.repeat(np.arange(n), deg)
+        crow, col = from_pairs(n, cols, r, rng.integers(0, cols, r.size))
+        return n, cols, crow, col
     if family == "powerlaw":  # Zipf degrees, uniform columns (configuration 2's shape)
         deg = np.minimum(rng.zipf(float(rng.uniform(1.5, 2.2)), n), min(n, 3000))
         deg[rng.random(n) < 0.1] = 0
@@ -114,7 +122,7 @@ def matrix(family, rng):
         r = np.repeat(np.arange(n), deg)
         c = rng.integers(0, n, r.size)
     crow, col = from_pairs(n, n, r, c)
-    return n, crow, col
+    return n, n, crow, col
 
 
 CASES = [(f, s) for s in range(8) for f in FAMILIES]
@@ -123,16 +131,16 @@ CASES = [(f, s) for s in range(8) for f in FAMILIES]
 @pytest.mark.parametrize("family,seed", CASES, ids=[f"{f}-{s}" for f, s in CASES])
 def test_sweep(spmm_npu, family, seed):
     rng = np.random.default_rng(1000 * seed + FAMILIES.index(family))
-    n, crow, col = matrix(family, rng)
+    n, cols, crow, col = matrix(family, rng)
     half = bool((seed + FAMILIES.index(family)) % 2)
     npdt = np.float16 if half else np.float32
     vals = rng.uniform(-1, 1, col.size).astype(npdt)
     widths = [16, 64, 128, 256, 512] + ([1024] if half else [])
-    N = int(rng.choice(widths[1:]))
-    B = rng.standard_normal((n, N)).astype(npdt)
+    N = int(rng.choice(widths[1:4] if family == "rect" else widths[1:]))
+    B = rng.standard_normal((cols, N)).astype(npdt)
     expected = O.spmm_f64(crow, col, vals, B)
     slack = accumulation_slack(crow, col, vals, B)
-    print(f"[sweep] {family} seed={seed} rows={n} nnz={col.size} N={N} {npdt.__name__}", flush=True)
+    print(f"[sweep] {family} seed={seed} rows={n} cols={cols} nnz={col.size} N={N} {npdt.__name__}", flush=True)
 
     # spmm_csr: tolerance, then width invariance on the first 16 columns.
     it = torch.int64 if seed % 2 else torch.int32
@@ -142,13 +150,16 @@ def test_sweep(spmm_npu, family, seed):
     narrow = spmm_npu.spmm_csr(dev(crow, it), dev(col, it), dev(vals), dev(np.ascontiguousarray(B[:, :16])), start)
     assert torch.equal(out[:, :16].cpu(), narrow.cpu()), "vector path differs across widths"
 
+    # The layout operators take int32 indices on even seeds, int64 on odd.
+    ix = np.int64 if seed % 2 else np.int32
+    crow_x, col_x = crow.astype(ix), col.astype(ix)
     i32 = torch.int32
     empty_i = torch.zeros(0, dtype=i32, device="cuda")
     empty_v = torch.zeros(0, dtype=dev(vals).dtype, device="cuda")
 
     # csr_to_bcsr: bit-exact layout, then the pure block part.
-    b = O.csr_to_bcsr(crow, col, vals, n, n, 16)
-    assert_same(spmm_npu.csr_to_bcsr(dev(crow), dev(col), dev(vals), n, n, 16), b)
+    b = O.csr_to_bcsr(crow_x, col_x, vals, n, cols, 16)
+    assert_same(spmm_npu.csr_to_bcsr(dev(crow_x), dev(col_x), dev(vals), n, cols, 16), b)
     out = spmm_npu.spmm_ascend_cube(dev(b["crow_window_ptr"], i32), dev(b["unique_col_ids"], i32), dev(b["value"]),
                                     torch.zeros(1, dtype=i32, device="cuda"), empty_i, empty_v, dev(B),
                                     dev(O.make_start(b["crow_window_ptr"], 20)),
@@ -157,19 +168,19 @@ def test_sweep(spmm_npu, family, seed):
 
     # block_level_split: bit-exact layout, then the mixed op.
     a = float(rng.choice([(222.0 / 190.0) * 0.5, 295.0 / 505.0, 0.1, 3.0]))
-    h = O.block_level_split(crow, col, vals, n, n, a, 16)
-    assert_same(spmm_npu.block_level_split(torch.from_numpy(crow), torch.from_numpy(col), torch.from_numpy(vals),
-                                           n, n, a, 16), h)
+    h = O.block_level_split(crow_x, col_x, vals, n, cols, a, 16)
+    assert_same(spmm_npu.block_level_split(torch.from_numpy(crow_x), torch.from_numpy(col_x), torch.from_numpy(vals),
+                                           n, cols, a, 16), h)
     out = spmm_npu.spmm_ascend_cube(
         dev(h["crow_window_ptr"], i32), dev(h["unique_col_ids"], i32), dev(h["value"]),
         dev(h["vrow_window_ptr"], i32), dev(h["vcol_indices"], i32), dev(h["vvalue"]), dev(B),
         dev(O.make_start(h["crow_window_ptr"], 20)), dev(O.make_start(h["vrow_window_ptr"], 40)))
     close(out[:n], expected, npdt, slack)
 
-    # preprocess, both layouts: bit-exact, then the mixed op on packed rows.
-    for graph_layout in (False, True):
-        p = O.preprocess(crow, col, vals, n, n, 16, graph_layout)
-        assert_same(spmm_npu.preprocess(dev(crow), dev(col), dev(vals), n, n, 16, graph_layout), p)
+    # preprocess: the graph layout needs a square matrix.
+    for graph_layout in (False, True) if n == cols else (False,):
+        p = O.preprocess(crow_x, col_x, vals, n, cols, 16, graph_layout)
+        assert_same(spmm_npu.preprocess(dev(crow_x), dev(col_x), dev(vals), n, cols, 16, graph_layout), p)
         ccol = p["renumbered_unique_col_ids"] if graph_layout else p["unique_col_ids"]
         vcol = p["renumbered_vcol_indices"] if graph_layout else p["vcol_indices"]
         inv = torch.from_numpy(p["inv_permutation"])
