@@ -11,7 +11,10 @@ families (one rectangular), each checked through every operator path against the
   on for square matrices only) bit for bit against the oracle's layouts,
   with int32 indices on even seeds and int64 on odd;
 * spmm_ascend_cube on each of those layouts against the fp64 product,
-  after restore_node_tensor where rows are packed.
+  after restore_node_tensor where rows are packed;
+* PackedGraph (graph layout, square families) forward against A x and
+  backward against A^T g, with the autograd test's bounds (4x the
+  tolerance for the gradient).
 
 The bound is the reference's atol = rtol (2e-2 fp16, 1e-4 fp32) plus the
 rounding that fp32 accumulation of a row's d products p_k admits in any
@@ -28,6 +31,7 @@ import pytest
 import torch
 
 import oracle as O
+from test_gpu_autograd import transpose_csr
 from test_gpu_preprocess import assert_same
 
 pytestmark = pytest.mark.gpu
@@ -41,8 +45,8 @@ def dev(a, dtype=None):
     return t if dtype is None else t.to(dtype)
 
 
-def close(out, expected, npdt, slack):
-    tol = TOL[npdt]
+def close(out, expected, npdt, slack, scale=1.0):
+    tol = TOL[npdt] * scale
     a = out.float().cpu().double().numpy()
     bad = np.abs(a - expected) > tol + tol * np.abs(expected) + slack
     assert not bad.any(), f"{int(bad.sum())} mismatches, max abs err {float(np.abs(a - expected).max()):.3e}"
@@ -192,3 +196,27 @@ def test_sweep(spmm_npu, family, seed):
             dev(p["vrow_window_ptr"], i32), dev(vcol, i32), dev(p["vvalue"]), dense,
             dev(O.make_start(p["crow_window_ptr"], 20)), dev(O.make_start(p["vrow_window_ptr"], 40)))
         close(spmm_npu.restore_node_tensor(out, inv), expected, npdt, slack)
+
+
+SQUARE_CASES = [(f, s) for s in range(4) for f in FAMILIES if f != "rect"]
+
+
+@pytest.mark.parametrize("family,seed", SQUARE_CASES, ids=[f"{f}-{s}" for f, s in SQUARE_CASES])
+def test_sweep_packed_graph(spmm_npu, family, seed):
+    rng = np.random.default_rng(7000 + 1000 * seed + FAMILIES.index(family))
+    n, _, crow, col = matrix(family, rng)
+    npdt, tdt = (np.float16, torch.float16) if seed % 2 else (np.float32, torch.float32)
+    vals = rng.uniform(0, 1, col.size).astype(npdt)
+    width = 32
+    print(f"[sweep-graph] {family} seed={seed} rows={n} nnz={col.size} {npdt.__name__}", flush=True)
+    prep = spmm_npu.preprocess(dev(crow), dev(col), dev(vals), n, n, 16, True)
+    G = spmm_npu.PackedGraph(prep)
+    x_np = rng.standard_normal((n, width)).astype(npdt)
+    w_np = rng.standard_normal((n, width)).astype(npdt)
+    x = torch.from_numpy(x_np).cuda().requires_grad_(True)
+    y = G.restore(G(G.pack(x)))
+    assert y.dtype == tdt
+    (y.float() * torch.from_numpy(w_np).cuda().float()).sum().backward()
+    close(y.detach(), O.spmm_f64(crow, col, vals, x_np), npdt, accumulation_slack(crow, col, vals, x_np))
+    tcrow, tcol, tval = transpose_csr(crow, col, vals, n)
+    close(x.grad, O.spmm_f64(tcrow, tcol, tval, w_np), npdt, accumulation_slack(tcrow, tcol, tval, w_np), 4.0)
