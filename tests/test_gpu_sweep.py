@@ -11,7 +11,8 @@ families (one rectangular), each checked through every operator path against the
   on for square matrices only) bit for bit against the oracle's layouts,
   with int32 indices on even seeds and int64 on odd;
 * spmm_ascend_cube on each of those layouts against the fp64 product,
-  after restore_node_tensor where rows are packed;
+  after restore_node_tensor where rows are packed, and the legacy
+  spmm_cube on the window encoding of the matrix;
 * PackedGraph (graph layout, square families) forward against A x and
   backward against A^T g, with the autograd test's bounds (4x the
   tolerance for the gradient).
@@ -168,6 +169,11 @@ def test_sweep(spmm_npu, family, seed):
                                     torch.zeros(1, dtype=i32, device="cuda"), empty_i, empty_v, dev(B),
                                     dev(O.make_start(b["crow_window_ptr"], 20)),
                                     torch.zeros(40, dtype=i32, device="cuda"))
+    close(out[:n], expected, npdt, slack)
+
+    # spmm_cube: the legacy window-encoded form of the same matrix.
+    rp, enc, ev = O.cube_encode(crow, col, vals, n)
+    out = spmm_npu.spmm_cube(dev(rp, it), dev(enc, it), dev(ev), dev(B), torch.zeros(20, dtype=i32, device="cuda"))
     close(out[:n], expected, npdt, slack)
 
     # block_level_split: bit-exact layout, then the mixed op.
