@@ -159,6 +159,36 @@ def time_calls(step, steps: int, warmup: int, cold: bool = False):
     return wall_ms, float(np.mean([a.elapsed_time(b) for a, b in ev]))
 
 
+def graph_ms(step, calls: int = 10, replays: int = 20) -> float:
+    """HIP-event ms per call when `calls` back-to-back calls are captured in
+    one HIP graph (torch.cuda.graph) and the graph is replayed `replays`
+    times: the per-call time without host launch overhead."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(calls):
+            step()
+    graph.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(replays):
+        graph.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / (replays * calls)
+    del graph
+    torch.cuda.synchronize()
+    return ms
+
+
 def device_csr(w, dev):
     return (torch.from_numpy(w.crow.astype(np.int32)).to(dev),
             torch.from_numpy(w.col.astype(np.int32)).to(dev),
@@ -438,6 +468,11 @@ def main() -> int:
         _, cold_ms = time_calls(step, min(args.steps, 10), 1, cold=True)
         log(f"[bench] cold-cache events {cold_ms:.4f} ms/call")
 
+    graph_call_ms = None
+    if args.op != "graph":  # the graph op's Python-side permutation checks read the device
+        graph_call_ms = graph_ms(step)
+        log(f"[bench] HIP graph replay {graph_call_ms:.4f} ms/call")
+
     copy_rate = copy_gbps(1 << 30, 5, 1)[1]
     log(f"[bench] 1 GiB device copy: {copy_rate:.1f} GB/s (read + write)")
 
@@ -470,6 +505,7 @@ def main() -> int:
         },
         "hbm_gbps_algorithmic": round(alg_bytes / t_s / 1e9, 1),
         "cold_cache_ms_per_call": None if cold_ms is None else round(cold_ms, 5),
+        "graph_replay_ms_per_call": None if graph_call_ms is None else round(graph_call_ms, 5),
         "roofline": {
             "bound": "hbm",
             "kernels": OP_KERNELS.get(args.op, ""),
