@@ -7,7 +7,11 @@ CPU: the oracle reproduces every vector, including the reference's error
 cases.  GPU: the HIP preprocess(graph_layout=True) reproduces the
 reference's renumbered ids, and its transpose_* keys are the fixed split
 (a = 295/505, extension/custom_op.cpp:1350-1384) of the reference's packed
-transpose."""
+transpose.  The window layout keys that graph.npz also holds
+(unique_col_ids, vcol_indices, inv_permutation) were written by the oracle
+and serve as the reference routines' inputs; the GPU's equality with them
+is a regression check, its pin is the oracle comparison of
+test_gpu_preprocess and the hand-worked cases of preprocess_cases."""
 
 import os
 
@@ -55,18 +59,22 @@ def test_renumber_golden():
 
 @pytest.mark.parametrize("i", [0, 1])
 def test_graph_layout_golden_oracle(i):
+    """graph.npz keeps, per matrix, the inputs the oracle's preprocess passed
+    to the reference routines (unique_col_ids, vcol_indices,
+    inv_permutation: written by the oracle, so they are inputs here, not
+    pins) and what the reference's own code returned for them (the
+    renumbered ids and the packed transpose: these are the pins)."""
     g = load("graph")
     crow, col, val = g[f"g{i}_crow"], g[f"g{i}_col"], g[f"g{i}_val"]
-    n = crow.size - 1
+    inv = g[f"g{i}_inv_permutation"]
     packed = int(g[f"g{i}_packed_rows"][0])
-    rt, ct, vt = O.transpose(crow, col, val, g[f"g{i}_inv_permutation"], packed)
+    rt, ct, vt = O.transpose(crow, col, val, inv, packed)
     np.testing.assert_array_equal(rt, g[f"g{i}_transpose_rowptr"])
     np.testing.assert_array_equal(ct, g[f"g{i}_transpose_col"])
     np.testing.assert_array_equal(vt.view(np.uint32), g[f"g{i}_transpose_val"].view(np.uint32))
-    pre = O.preprocess(crow, col, val, n, n, 16, True)
-    for key in ("unique_col_ids", "vcol_indices", "inv_permutation", "renumbered_unique_col_ids",
-                "renumbered_vcol_indices"):
-        np.testing.assert_array_equal(pre[key].astype(np.int64), g[f"g{i}_{key}"], err_msg=key)
+    for src, out in (("unique_col_ids", "renumbered_unique_col_ids"), ("vcol_indices", "renumbered_vcol_indices")):
+        got = O.renumber(g[f"g{i}_{src}"], inv, np.int64)
+        np.testing.assert_array_equal(got, g[f"g{i}_{out}"], err_msg=out)
 
 
 @pytest.mark.gpu

@@ -71,7 +71,7 @@ def test_packed_graph_forward_and_backward(spmm_npu, dtype, seed, n, deg):
                                atol=tol, rtol=tol)
     tcrow, tcol, tval = transpose_csr(crow, col, val, n)
     np.testing.assert_allclose(x.grad.double().cpu().numpy(), O.spmm_f64(tcrow, tcol, tval, w_np),
-                               atol=tol * 4, rtol=tol * 4)
+                               atol=tol, rtol=tol)
 
 
 def test_packed_graph_rejects_unpacked_layout(spmm_npu):

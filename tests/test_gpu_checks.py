@@ -96,3 +96,35 @@ def test_failure_exits_nonzero(spmm_npu, dataset_dir, tmp_path, monkeypatch):
                 "--output", str(out)])
     r = report(out)
     assert r["passed"] is False and r["failed"] == 1 and "first_mismatch_row" in r["cases"][0]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("method", ["ours", "naive", "neutronsparse", "block-split"])
+def test_partitions_match_fp64(spmm_npu, dataset_dir, dtype, method):
+    """Every partition of the task-mapping comparison (tests/task_mapping/
+    common.py:146-347), run through spmm_ascend_cube (run_mapping), against
+    the fp64 oracle product at the reference's tolerance, on both datasets
+    and at two widths; the naive split also at fractions 0 and 1 (all
+    vector, all block)."""
+    import oracle as O
+    import partition as PT
+
+    tol = 2e-2 if dtype == torch.float16 else 1e-4
+    for path in sorted(dataset_dir.rglob("*.pt")):
+        name, rows, cols, crow, col = D.load_payload(path)
+        seed = D.stable_seed(2027, path.relative_to(dataset_dir).as_posix())
+        values = D.make_values(col.numel(), dtype, seed)
+        fractions = (PT.DEFAULT_NAIVE_FRACTION, 0.0, 1.0) if method == "naive" else (PT.DEFAULT_NAIVE_FRACTION,)
+        for fraction in fractions:
+            mapping, meta = PT.prepare_partition(method, rows, cols, crow, col, values, naive_fraction=fraction)
+            assert meta["aic_nnz"] + meta["aiv_nnz"] == col.numel()
+            if method != "ours":
+                assert meta["aic_nnz"] > 0 or method == "neutronsparse" or fraction == 0.0
+            for dim in (16, 128):
+                dense = D.make_dense(cols, dim, dtype, seed + dim)
+                out = PT.run_mapping(mapping, dense.cuda(), rows)
+                expected = O.spmm_f64(crow.numpy(), col.numpy(), values.numpy(), dense.numpy())
+                err = np.abs(out.double().cpu().numpy() - expected)
+                bad = err > tol + tol * np.abs(expected)
+                assert not bad.any(), (f"{name} {method} fraction={fraction} N={dim}: {int(bad.sum())} "
+                                       f"mismatches, max abs err {float(err.max()):.3e}")

@@ -8,6 +8,7 @@ import pytest
 import torch
 
 import oracle as O
+import preprocess_cases as PC
 import workloads as W
 
 pytestmark = pytest.mark.gpu
@@ -201,3 +202,19 @@ def test_preprocessing_errors(spmm_npu):
     crow = np.array([0] + [17] * 16, np.int64)
     with pytest.raises(ValueError, match="coalesce duplicate CSR entries"):
         spmm_npu.preprocess(t(crow), t(np.zeros(17, np.int64)), t(np.ones(17, np.float32)), 16, 4)
+
+
+@pytest.mark.parametrize("name", sorted(PC.CASES))
+@pytest.mark.parametrize("graph_layout", [False, True])
+def test_preprocess_hand_worked_order_and_tie(spmm_npu, name, graph_layout):
+    """The hand-worked cases of preprocess_cases (vector windows in density
+    order; an exact tie at the >= marginal test) on the GPU pipeline: the
+    hand-derived fields, and every key bit for bit against the oracle."""
+    crow, col, val, expected = PC.CASES[name]()
+    n = expected["nrows"]
+    for index_dtype in (np.int32, np.int64):
+        c, k = crow.astype(index_dtype), col.astype(index_dtype)
+        got = spmm_npu.preprocess(torch.from_numpy(c).cuda(), torch.from_numpy(k).cuda(), torch.from_numpy(val).cuda(),
+                                  n, n, 16, graph_layout)
+        PC.check_against_hand({key: t.cpu().numpy() for key, t in got.items()}, crow, col, expected)
+        assert_same(got, O.preprocess(c, k, val, n, n, 16, graph_layout))

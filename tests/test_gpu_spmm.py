@@ -485,27 +485,30 @@ def test_invalid_columns_and_nonfinite_values_stay_in_their_rows(spmm_npu):
         assert bool(torch.isclose(out[finite], e[finite], atol=1e-4, rtol=1e-4).all())
 
 
-def test_dense_operand_beyond_32bit_extent(spmm_npu):
-    """A dense operand larger than 4 GB (fp32, K = 2.2M rows of N = 512)
-    takes the 64-bit global-load path; columns in the last rows are read."""
-    K, N, rows = 2_200_000, 512, 600
+@pytest.mark.parametrize("dtype,N", [("fp32", 512), ("fp16", 1024)])
+def test_dense_operand_beyond_32bit_extent(spmm_npu, dtype, N):
+    """A dense operand larger than 4 GB (K = 2.2M rows; fp32 N = 512 or fp16
+    N = 1024) takes the gather's 64-bit global-load path; columns in the
+    last rows are read."""
+    K, rows = 2_200_000, 600
+    tdt = torch.float32 if dtype == "fp32" else torch.float16
     rng = np.random.default_rng(73)
-    B = torch.empty((K, N), dtype=torch.float32, device="cuda")
+    B = torch.empty((K, N), dtype=tdt, device="cuda")
     B.normal_(generator=torch.Generator(device="cuda").manual_seed(5))
-    assert K * N * 4 > 0xFFFFF000
+    assert K * N * B.element_size() > 0xFFFFF000
     deg = rng.integers(0, 20, rows)
     crow = np.zeros(rows + 1, np.int64)
     crow[1:] = np.cumsum(deg)
     col = np.concatenate([np.sort(rng.choice(K, d, replace=False)) for d in deg]).astype(np.int64)
     col[:50] = np.sort(rng.choice(np.arange(K - 1000, K), 50, replace=False))  # the far end of B
     col[60] = K + 1  # invalid
-    vals = rng.uniform(-1, 1, col.size).astype(np.float32)
+    vals = rng.uniform(-1, 1, col.size).astype(NP_DT[dtype])
     out = spmm_npu.spmm_csr(dev(crow, torch.int32), dev(col, torch.int32), dev(vals), B,
                             dev(O.make_start(crow, 40)))
     used = np.unique(col[col < K])
     Bsub = B[torch.from_numpy(used).cuda()].cpu().numpy()
     remap = np.where(col < K, np.searchsorted(used, np.minimum(col, K - 1)), used.size + 5)
-    assert_close(out, O.spmm_f64(crow, remap, vals, Bsub), "fp32")
+    assert_close(out, O.spmm_f64(crow, remap, vals, Bsub), dtype)
     del B
     torch.cuda.empty_cache()
 

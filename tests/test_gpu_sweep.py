@@ -14,17 +14,19 @@ families (one rectangular), each checked through every operator path against the
   after restore_node_tensor where rows are packed, and the legacy
   spmm_cube on the window encoding of the matrix;
 * PackedGraph (graph layout, square families) forward against A x and
-  backward against A^T g, with the autograd test's bounds (4x the
-  tolerance for the gradient).
+  backward against A^T g, at the same bound.
 
-The bound is the reference's atol = rtol (2e-2 fp16, 1e-4 fp32) plus the
-rounding that fp32 accumulation of a row's d products p_k admits in any
-order: 4 u sqrt(d) sqrt(sum p_k^2), u = 2^-24 (about ten standard
-deviations of recursive summation's error, whose size is u n sigma for n
-terms of rms sigma).  It matters only for the hub rows of tens of thousands
-of nonzeros, where no fp32 summation order stays inside 1e-4 (a sequential
-fp32 sum of those rows misses it too); for rows of ordinary degree it is a
-small fraction of the reference's tolerance.
+The bound is the reference's atol = rtol (2e-2 fp16, 1e-4 fp32) for every
+row of at most SLACK_DEGREE (1024) nonzeros.  Rows longer than that (the
+hub rows, up to tens of thousands of nonzeros) also get the rounding that
+fp32 accumulation of d products p_k admits in any order,
+4 u sqrt(d) sqrt(sum p_k^2), u = 2^-24 (about ten standard deviations of
+recursive summation's error, whose size is u n sigma for n terms of rms
+sigma): there no fp32 summation order stays inside 1e-4 where the result
+cancels to near zero (a sequential fp32 CPU sum of those rows misses it
+too).  For d <= 1024 and the U(-1, 1) x N(0, 1) products used here, that
+error is about 2.4e-8 d rms, under a quarter of the fp32 tolerance, so
+ordinary rows are held to the plain bound.
 """
 
 import numpy as np
@@ -46,19 +48,23 @@ def dev(a, dtype=None):
     return t if dtype is None else t.to(dtype)
 
 
-def close(out, expected, npdt, slack, scale=1.0):
-    tol = TOL[npdt] * scale
+def close(out, expected, npdt, slack):
+    tol = TOL[npdt]
     a = out.float().cpu().double().numpy()
     bad = np.abs(a - expected) > tol + tol * np.abs(expected) + slack
     assert not bad.any(), f"{int(bad.sum())} mismatches, max abs err {float(np.abs(a - expected).max()):.3e}"
 
 
+SLACK_DEGREE = 1024
+
+
 def accumulation_slack(crow, col, vals, B):
-    """4 u sqrt(d_r) sqrt(sum_k (a_rk B_kj)^2) per output element, u = 2^-24."""
+    """4 u sqrt(d_r) sqrt(sum_k (a_rk B_kj)^2) per output element of a row
+    of d_r > SLACK_DEGREE nonzeros, u = 2^-24; zero for every other row."""
     v = vals.astype(np.float64)
     d = np.diff(crow).astype(np.float64)[:, None]
     s2 = O.spmm_f64(crow, col, v * v, B.astype(np.float64) ** 2)
-    return 4.0 * 2.0 ** -24 * np.sqrt(d) * np.sqrt(s2)
+    return np.where(d > SLACK_DEGREE, 4.0 * 2.0 ** -24 * np.sqrt(d) * np.sqrt(s2), 0.0)
 
 
 def from_pairs(rows, cols, r, c):
@@ -225,4 +231,4 @@ def test_sweep_packed_graph(spmm_npu, family, seed):
     (y.float() * torch.from_numpy(w_np).cuda().float()).sum().backward()
     close(y.detach(), O.spmm_f64(crow, col, vals, x_np), npdt, accumulation_slack(crow, col, vals, x_np))
     tcrow, tcol, tval = transpose_csr(crow, col, vals, n)
-    close(x.grad, O.spmm_f64(tcrow, tcol, tval, w_np), npdt, accumulation_slack(tcrow, tcol, tval, w_np), 4.0)
+    close(x.grad, O.spmm_f64(tcrow, tcol, tval, w_np), npdt, accumulation_slack(tcrow, tcol, tval, w_np))

@@ -58,23 +58,63 @@ def _distinct_rows(rng: np.random.Generator, degrees: np.ndarray, cols: int):
     rows = degrees.size
     r = np.repeat(np.arange(rows, dtype=np.int64), degrees)
     c = rng.integers(0, cols, size=r.size, dtype=np.int64)
-    for _ in range(8):  # redraw rows that drew a repeated column
-        key = r * cols + c
-        order = np.argsort(key, kind="stable")
-        ks = key[order]
-        dup = np.zeros(ks.size, dtype=bool)
-        dup[1:] = ks[1:] == ks[:-1]
-        if not dup.any():
-            break
-        bad = order[dup]
-        c[bad] = rng.integers(0, cols, size=bad.size, dtype=np.int64)
+    crow = np.concatenate([[0], np.cumsum(degrees)]).astype(np.int64)
+    # Rows holding more than half the columns (only in scaled-down matrices)
+    # are drawn without replacement: redrawing their repeats would take long.
+    for row in np.nonzero(degrees > cols // 2)[0]:
+        c[crow[row]:crow[row + 1]] = rng.choice(cols, int(degrees[row]), replace=False)
+    c = _redraw_duplicates(rng, r, c, cols, crow,
+                           lambda idx, final: rng.integers(0, cols, size=idx.size, dtype=np.int64))
     return _csr_from_coo(rows, r, c, cols)
 
 
 def _zipf_degrees(rng, rows, alpha, max_deg, target_nnz):
-    d = np.minimum(rng.zipf(alpha, size=rows), max_deg).astype(np.float64)
-    d = np.clip(np.rint(d * (target_nnz / d.sum())), 1, max_deg)
-    return d.astype(np.int64)
+    """Zipf(alpha) degrees clipped to [1, max_deg], then rescaled (scale,
+    round, re-clip) so that they sum to target_nnz.  Rounding and the clip at
+    either end move the sum off a plain target/sum factor (at config 2's
+    factor of about 1.3 every degree-1 row rounds back to 1, losing 6.6%), so
+    the factor is found by bisection on the rescaled sum, which is monotone
+    in it; the sum lands within a few degrees of the target."""
+    d0 = np.minimum(rng.zipf(alpha, size=rows), max_deg).astype(np.float64)
+
+    def total(f):
+        return np.clip(np.rint(d0 * f), 1, max_deg).sum()
+
+    lo, hi = 0.0, target_nnz / d0.sum()
+    while total(hi) < target_nnz and hi < 1e9:
+        hi *= 2
+    for _ in range(60):  # smallest factor whose sum reaches the target
+        mid = 0.5 * (lo + hi)
+        lo, hi = (mid, hi) if total(mid) < target_nnz else (lo, mid)
+    return np.clip(np.rint(d0 * hi), 1, max_deg).astype(np.int64)
+
+
+def _row_ranges(crow: np.ndarray, rows: np.ndarray) -> np.ndarray:
+    """Positions of the entries of the given rows (CSR row pointer crow)."""
+    starts, lens = crow[rows], crow[rows + 1] - crow[rows]
+    if lens.sum() == 0:
+        return np.zeros(0, np.int64)
+    offs = np.repeat(starts - np.concatenate([[0], np.cumsum(lens)[:-1]]), lens)
+    return offs + np.arange(int(lens.sum()), dtype=np.int64)
+
+
+def _redraw_duplicates(rng, r, c, cols, crow, redraw, rounds=6):
+    """Redraws every repeated (row, column) pair until each row's columns are
+    distinct.  r is sorted (row-major entries, row pointer crow); redraw(idx,
+    final) returns new columns for positions idx, with final=True after
+    `rounds` rounds (the caller then draws from a larger space).  Only the rows that still hold a repeat are re-checked."""
+    idx = np.arange(r.size, dtype=np.int64)
+    for it in range(10 * rounds):
+        key = r[idx] * cols + c[idx]
+        order = np.argsort(key, kind="stable")
+        ks = key[order]
+        dup = ks[1:] == ks[:-1]
+        if not dup.any():
+            return c
+        bad = idx[order[1:][dup]]
+        c[bad] = redraw(bad, it >= rounds)
+        idx = _row_ranges(crow, np.unique(r[bad]))
+    raise RuntimeError("duplicate columns could not be redrawn")
 
 
 def config1(scale: float = 1.0) -> Workload:
@@ -151,7 +191,12 @@ def config4(scale: float = 1.0) -> Workload:
 
 def config5(scale: float = 1.0) -> Workload:
     """Graph-like 1048576^2 (~32M nnz): Zipf(2.0) degrees in [1, 8192], 70% of
-    edges inside 4096-node communities, random relabelling; fp32, N=512."""
+    edges inside 4096-node communities, random relabelling; fp32, N=512.
+    Repeated columns of a row are redrawn, so the rows keep their drawn
+    degrees and nnz is the rescaled degree sum (32.0M at full size).  Rows of
+    more than 4096 community edges cannot hold them all distinct, and the
+    repeats that are still left after a few community redraws are drawn
+    globally."""
     seed = 2027 + 5
     rng = np.random.default_rng(seed)
     n = max(4096, int(1048576 * scale))
@@ -164,6 +209,19 @@ def config5(scale: float = 1.0) -> Workload:
     c[local] = base[local] + rng.integers(0, comm, size=int(local.sum()), dtype=np.int64)
     c[~local] = rng.integers(0, n, size=int((~local).sum()), dtype=np.int64)
     c = np.minimum(c, n - 1)
+
+    def redraw(idx, final):
+        # A repeated column is drawn again the way it was drawn (inside the
+        # row's community or globally); a row holding more community edges
+        # than its community has nodes draws the rest globally.
+        out = rng.integers(0, n, size=idx.size, dtype=np.int64)
+        if not final:
+            loc = local[idx]
+            out[loc] = base[idx[loc]] + rng.integers(0, comm, size=int(loc.sum()), dtype=np.int64)
+        return np.minimum(out, n - 1)
+
+    crow0 = np.concatenate([[0], np.cumsum(deg)]).astype(np.int64)
+    c = _redraw_duplicates(rng, r, c, n, crow0, redraw)
     q = rng.permutation(n).astype(np.int64)  # node relabelling Q
     crow, col = _csr_from_coo(n, q[r], q[c], n)
     vals = rng.uniform(0, 1, col.size).astype(np.float32)
