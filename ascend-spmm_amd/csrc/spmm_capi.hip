@@ -3,9 +3,19 @@
 // operator contracts (extension/custom_op.cpp:36-152) at the level of sizes
 // and dtypes; tensor-level checks (device, rank, contiguity) live in the torch
 // extension that calls this library.
+#include <mutex>
 #include <string>
 
 #include "common.h"
+
+// Scratch of spmm_csr_run_noalloc: the gather workspace (tail rows and fp32
+// partial slots) of callers that cannot allocate.  Each device that loads
+// the library holds its own copy until the process ends.  Host code must not
+// pass this name to a kernel (on the host it is a stand-in, not a device
+// address): its per-device address comes from hipGetSymbolAddress, once per
+// device (scratch_on_current_device below).
+constexpr size_t kNoallocScratchBytes = size_t(64) << 20;
+static __device__ __align__(256) unsigned char scratch[kNoallocScratchBytes];
 
 namespace spmm {
 
@@ -62,6 +72,49 @@ spmm_status check_aligned(const void* dense, const void* out, const char* op) {
   return SPMM_OK;
 }
 
+// Checks shared by spmm_csr_run and its allocation-free variant (everything
+// before the pointers).
+spmm_status check_csr_desc(const spmm_csr_desc* d, const char* op) {
+  if (d == nullptr) return fail(SPMM_ERR_INVALID_ARGUMENT, "null descriptor");
+  if (spmm_status st = check_types(d->index_type, d->value_type, op)) return st;
+  if (spmm_status st = check_width(d->width, d->value_type, d->value_type == SPMM_VALUE_F16 ? 16 : 8, op))
+    return st;
+  if (d->rows < 0 || d->nnz < 0 || d->dense_rows < 0)
+    return fail(SPMM_ERR_CONTRACT, std::string(op) + ": negative extent");
+  return SPMM_OK;
+}
+
+spmm_status check_csr_pointers(const spmm_csr_desc* d, const void* rowptr, const void* col,
+                               const void* value, const void* dense, void* out, const char* op) {
+  if (rowptr == nullptr || out == nullptr || (d->nnz > 0 && (col == nullptr || value == nullptr)) ||
+      (d->dense_rows > 0 && dense == nullptr))
+    return fail(SPMM_ERR_INVALID_ARGUMENT, std::string(op) + ": null device pointer");
+  return check_aligned(dense, out, op);
+}
+
+// Device address of `scratch` on the current device, resolved with
+// hipGetSymbolAddress on the first call per device (with that device
+// current) and kept; every later call on the device reuses it.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch[kMaxDevices] = {};
+
+spmm_status scratch_on_current_device(void** ptr) {
+  int dev = -1;
+  if (spmm_status st = check_hip(hipGetDevice(&dev), "hipGetDevice")) return st;
+  if (dev < 0 || dev >= kMaxDevices) return fail(SPMM_ERR_DEVICE, "device ordinal out of range");
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch[dev] == nullptr) {
+    void* p = nullptr;
+    if (spmm_status st = check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)"))
+      return st;
+    if (p == nullptr) return fail(SPMM_ERR_DEVICE, "hipGetSymbolAddress(scratch) returned null");
+    g_scratch[dev] = p;
+  }
+  *ptr = g_scratch[dev];
+  return SPMM_OK;
+}
+
 }  // namespace
 }  // namespace spmm
 
@@ -85,20 +138,36 @@ spmm_status spmm_csr_run(const spmm_csr_desc* d, const void* rowptr, const void*
                          const void* value, const void* dense, void* out, void* workspace,
                          size_t workspace_bytes, spmm_stream stream) {
   clear_error();
-  if (d == nullptr) return fail(SPMM_ERR_INVALID_ARGUMENT, "null descriptor");
-  if (spmm_status st = check_types(d->index_type, d->value_type, "spmm_csr")) return st;
-  if (spmm_status st = check_width(d->width, d->value_type,
-                                   d->value_type == SPMM_VALUE_F16 ? 16 : 8, "spmm_csr"))
-    return st;
-  if (d->rows < 0 || d->nnz < 0 || d->dense_rows < 0)
-    return fail(SPMM_ERR_CONTRACT, "spmm_csr: negative extent");
+  if (spmm_status st = check_csr_desc(d, "spmm_csr")) return st;
   if (d->rows == 0) return SPMM_OK;
-  if (rowptr == nullptr || out == nullptr || (d->nnz > 0 && (col == nullptr || value == nullptr)) ||
-      (d->dense_rows > 0 && dense == nullptr))
-    return fail(SPMM_ERR_INVALID_ARGUMENT, "spmm_csr: null device pointer");
-  if (spmm_status st = check_aligned(dense, out, "spmm_csr")) return st;
+  if (spmm_status st = check_csr_pointers(d, rowptr, col, value, dense, out, "spmm_csr")) return st;
   return launch_gather(d->index_type, d->value_type, rowptr, col, value, d->nnz, d->rows, 0, d->rows,
                        dense, d->dense_rows, d->width, out, workspace, workspace_bytes, nullptr, 0, 0,
+                       nullptr, nullptr, nullptr, as_stream(stream));
+}
+
+size_t spmm_csr_noalloc_max_scratch(void) { return kNoallocScratchBytes; }
+
+spmm_status spmm_csr_run_noalloc(const spmm_csr_desc* d, const void* rowptr, const void* col,
+                                 const void* value, const void* dense, void* out, spmm_stream stream) {
+  clear_error();
+  if (spmm_status st = check_csr_desc(d, "spmm_csr_run_noalloc")) return st;
+  // The gather's scratch (tail rows, fp32 partial slots) must fit the fixed
+  // array; checked before any HIP call.
+  const size_t need = gather_workspace_bytes(d->nnz, d->width);
+  if (need > kNoallocScratchBytes)
+    return fail(SPMM_ERR_CONTRACT, "spmm_csr_run_noalloc: this call needs " + std::to_string(need) +
+                                       " bytes of scratch, more than the library's fixed " +
+                                       std::to_string(kNoallocScratchBytes) +
+                                       "; call spmm_csr_run with a workspace instead");
+  if (d->rows == 0) return SPMM_OK;
+  if (spmm_status st = check_csr_pointers(d, rowptr, col, value, dense, out, "spmm_csr_run_noalloc")) return st;
+  void* ws = nullptr;
+  if (spmm_status st = scratch_on_current_device(&ws)) return st;
+  // Nothing in the scratch needs clearing: every call writes each tail entry
+  // and each partial slot before the post pass reads it.
+  return launch_gather(d->index_type, d->value_type, rowptr, col, value, d->nnz, d->rows, 0, d->rows,
+                       dense, d->dense_rows, d->width, out, ws, kNoallocScratchBytes, nullptr, 0, 0,
                        nullptr, nullptr, nullptr, as_stream(stream));
 }
 

@@ -93,6 +93,23 @@ spmm_status spmm_csr_run(const spmm_csr_desc* desc,
                          void* workspace, size_t workspace_bytes,
                          spmm_stream stream);
 
+/* Allocation-free spmm_csr: same arguments (minus the workspace), same
+ * kernels and bit-identical results as spmm_csr_run.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Its scratch is a fixed device array inside the library, of
+ * spmm_csr_noalloc_max_scratch() bytes (64 MiB) per GPU, held from the
+ * library's load until the process ends; the call allocates nothing.  A call
+ * whose scratch (spmm_csr_workspace's figure) exceeds it fails with
+ * SPMM_ERR_CONTRACT before touching the device.  Every call on one GPU shares
+ * that GPU's array, so calls that overlap on one GPU (different streams, or
+ * host threads, without ordering between them) race and must not be made. */
+size_t spmm_csr_noalloc_max_scratch(void);
+
+spmm_status spmm_csr_run_noalloc(const spmm_csr_desc* desc,
+                                 const void* rowptr, const void* col, const void* value,
+                                 const void* dense, void* out, spmm_stream stream);
+
 /* Thread-per-row scalar CSR SpMM, same arguments and result contract as
  * spmm_csr_run (same sums in the same order within a row; no workspace).
  * No counterpart in the reference: it is the baseline that the block path's

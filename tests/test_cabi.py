@@ -81,6 +81,11 @@ def test_host_validation_without_gpu(lib):
     m.block_windows = 10
     assert lib.spmm_mixed_out_rows(ctypes.byref(m)) == 160
     assert lib.spmm_pack_workspace(ctypes.c_int64(100)) == 800
+    # the allocation-free spmm_csr rejects a call whose scratch exceeds its
+    # fixed array before any device call (40M nonzeros at fp16 N=1024)
+    d = CsrDesc(1000, 40_000_000, 1000, 1024, 0, 0)
+    assert lib.spmm_csr_run_noalloc(ctypes.byref(d), None, None, None, None, None, None) == 4
+    assert b"more than the library's fixed" in lib.spmm_last_error()
 
 
 @pytest.mark.gpu
