@@ -65,13 +65,16 @@ inline int64_t gather_slot_floats(int64_t width) { return (width + 63) / 64 * 64
 // With a block part (Crowptr != nullptr, cwin windows, climit usable blocks),
 // the vector sums of rows in block windows with blocks go to `vpart` (fp32)
 // instead of `out`, and their empty rows are left to the block kernel.
+// `zero_counts` (count entries, may be null) is zeroed by the post pass, for
+// the block kernel that runs next.
 spmm_status launch_gather(int32_t index_type, int32_t value_type,
                           const void* rowptr, const void* col, const void* value,
                           int64_t nnz, int64_t vrows, int64_t row_lo, int64_t row_hi,
                           const void* dense, int64_t dense_rows, int64_t width,
                           void* out, void* workspace, size_t workspace_bytes,
                           const void* Crowptr, int64_t cwin, int64_t climit, float* vpart,
-                          const void* Ccol, int32_t* order, hipStream_t stream);
+                          const void* Ccol, int32_t* order, uint32_t* zero_counts, int64_t count,
+                          hipStream_t stream);
 
 // Locality order of the block windows: with `order` set, one extra
 // work-group of the gather kernel, running beside the gathers, sorts the cwin
@@ -96,13 +99,15 @@ spmm_status launch_rowscalar(int32_t index_type, int32_t value_type, const void*
 size_t gather_workspace_bytes(int64_t nnz, int64_t width);
 
 // Blocks of a window handled by one work-group before the window is split
-// into chunks that separate work-groups sum and a combine pass adds in
+// into chunks that separate work-groups sum and the last of them adds in
 // order.  Large enough that ordinary windows are never split (each overflow
 // range costs a work-group and a window search), and growing with the total
 // block count (at most about 16384 chunks, 4096 blocks per chunk at most),
 // so large inputs keep the partial sums (and their workspace) small; it
 // depends on the value type and the block count only, never on the width,
-// so results do not depend on the width.
+// so results do not depend on the width.  fp32 keeps 1024: the split also
+// bounds the fp32 accumulation chain of hub rows (config 5's rows of 8192
+// nonzeros miss the 1e-4 tolerance in 44 of 35M sampled elements with 4096).
 inline int64_t block_chunk_for(int32_t value_type, int64_t blocks) {
   int64_t k = value_type == SPMM_VALUE_F16 ? 2048 : 1024;
   while (k < 4096 && blocks / k > 16384) k *= 2;
@@ -116,13 +121,16 @@ int64_t block_overflow_ranges(int64_t blocks, int64_t kbig);
 // blocks is written to `out` as block sum + the fp32 vector sums the gather
 // pass left in `vpart` ([16*windows][width]) for its rows with vector
 // nonzeros, rounded once.  `slots` holds the pieces of windows longer than
-// block_chunk ([ranges][2][16][width] fp32).
+// block_chunk ([ranges][2][16][width] fp32) followed by one uint32 counter per
+// range (block_counter_offset), which must be zero when the block kernel
+// starts: zeroed by the gather's post pass when it runs in the same call
+// (launch_gather's zero_counts), else by launch_block itself (zero_counts).
 spmm_status launch_block(int32_t index_type, int32_t value_type,
                          const void* Crowptr, const void* Ccol, const void* Cvalue,
                          int64_t windows, int64_t block_count, int64_t block_values,
                          const void* Vrowptr, int64_t vector_rows, int64_t vector_nnz,
                          const void* dense, int64_t dense_rows, int64_t width,
                          void* out, const float* vpart, float* slots, const int32_t* order,
-                         hipStream_t stream);
+                         bool zero_counts, hipStream_t stream);
 
 }  // namespace spmm

@@ -33,8 +33,11 @@
 //  * Windows longer than a chunk (block_chunk_for: 2048 blocks fp16, 1024
 //    fp32, growing with the total block count) are cut at fixed block
 //    positions: the window's own work-group takes its first chunk, and "overflow" work-groups take the rest in fixed
-//    global block ranges (only one window can overflow into a range).  A
-//    combine kernel adds the pieces in order, so the split is deterministic.
+//    global block ranges (only one window can overflow into a range).  Each
+//    piece's work-group stores its fp32 sum and counts itself on the
+//    window's counter; the one that completes the count adds the pieces in
+//    order (first chunk, then the overflow ranges), so the split is
+//    deterministic and needs no combine launch.
 //  * Vector (CSR) nonzeros of rows inside block windows are summed by the CSR
 //    gather kernel first (so long rows get its load balance) and left in an
 //    fp32 workspace; the block kernel adds them after the block sum and
@@ -98,7 +101,7 @@ struct BlockArgs {
   T* out;
   const float* vpart;      // [16*windows][N] fp32 vector sums of block-window rows (gather pass)
   float* slots;            // [noverflow][2][16][N] fp32 partials of windows longer than kbig
-  int64_t* first_of;       // [noverflow]: window whose blocks past its first chunk start in range k, or -1
+  uint32_t* cnt;           // [noverflow]: pieces stored so far of the window whose second chunk starts in range k
   int64_t kbig, noverflow, per_xcd;
   int64_t stage;           // blocks staged in LDS at a time (multiple of the K-step)
   int zero_empty;          // no vector part: windows without blocks write their rows as zeros
@@ -385,9 +388,15 @@ __device__ inline void window_chunk(const BlockArgs<T, I>& a, int64_t s, int64_t
 #pragma unroll
       for (int j = 0; j < C; ++j) v[j] = acc[j][e];
       if (slot) {
+        // Read by another work-group, possibly on another XCD: agent-scope
+        // atomic stores, performed coherently across the XCDs' L2s.
 #pragma unroll
-        for (int w = 0; w < C; w += 4)
-          *reinterpret_cast<float4_t*>(slot + o + w) = float4_t{v[w], v[w + 1], v[w + 2], v[w + 3]};
+        for (int w = 0; w < C; w += 2) {
+          const uint64_t bits = static_cast<uint64_t>(__float_as_uint(v[w])) |
+                                (static_cast<uint64_t>(__float_as_uint(v[w + 1])) << 32);
+          __hip_atomic_store(reinterpret_cast<uint64_t*>(slot + o + w), bits, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+        }
         continue;
       }
       if (vec >> r & 1u) {
@@ -401,6 +410,89 @@ __device__ inline void window_chunk(const BlockArgs<T, I>& a, int64_t s, int64_t
       store_cols<T, C>(out_w + o, v);
     }
   }
+}
+
+// A window of blocks [b0, b1), longer than kbig, is summed in pieces: its own
+// work-group's first chunk (slot (k0, 1), k0 = (b0 + kbig) / kbig) and one
+// segment per overflow range k0 .. k_end (slot (k, 0)).  After storing its
+// piece, a work-group counts itself on cnt[k0]; the one that completes the
+// count adds first chunk + segments k0, k0+1, ... in order, adds the rows'
+// vector sums, rounds once and writes the window's 16 rows, then resets the
+// counter to zero for the next call.  All threads of the work-group call it.
+template <typename T, typename I>
+__device__ inline void settle_window(const BlockArgs<T, I>& a, int64_t s, int64_t b0, int64_t b1) {
+  __shared__ uint32_t s_last;
+  const int64_t k0 = (b0 + a.kbig) / a.kbig;
+  const int64_t k_end = (b1 - 1) / a.kbig;
+  // This work-group's piece stores are complete (performed at agent scope)
+  // before the count that publishes them.
+  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t old = __hip_atomic_fetch_add(a.cnt + k0, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = static_cast<int64_t>(old) + 1 == k_end - k0 + 2 ? 1u : 0u;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  const int64_t n = 16 * a.N;
+  auto load4 = [](const float* p) {
+    lanes::float4_t f;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint64_t bits = __hip_atomic_load(reinterpret_cast<const uint64_t*>(p) + h, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+      f[2 * h] = __uint_as_float(static_cast<uint32_t>(bits));
+      f[2 * h + 1] = __uint_as_float(static_cast<uint32_t>(bits >> 32));
+    }
+    return f;
+  };
+  // Each thread keeps kIt groups of 4 elements and walks the pieces in order,
+  // the next piece's loads in flight while the current one is added: about
+  // one round trip per piece.
+  constexpr int kIt = 4;
+  const int64_t stride = 4 * static_cast<int64_t>(blockDim.x);
+  for (int64_t base = 4 * static_cast<int64_t>(threadIdx.x); base < n; base += kIt * stride) {
+    lanes::float4_t acc[kIt], nxt[kIt];
+#pragma unroll
+    for (int t = 0; t < kIt; ++t) {
+      const int64_t i = base + t * stride < n ? base + t * stride : base;
+      acc[t] = load4(a.slots + (2 * k0 + 1) * n + i);
+      nxt[t] = load4(a.slots + (2 * k0) * n + i);
+    }
+    for (int64_t q = k0; q <= k_end; ++q) {
+      lanes::float4_t cur[kIt];
+#pragma unroll
+      for (int t = 0; t < kIt; ++t) cur[t] = nxt[t];
+      if (q < k_end) {
+#pragma unroll
+        for (int t = 0; t < kIt; ++t) {
+          const int64_t i = base + t * stride < n ? base + t * stride : base;
+          nxt[t] = load4(a.slots + (2 * (q + 1)) * n + i);
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < kIt; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[t][e] = acc[t][e] + cur[t][e];
+    }
+#pragma unroll
+    for (int t = 0; t < kIt; ++t) {
+      const int64_t i = base + t * stride;
+      if (i >= n) break;
+      const int64_t r = i / a.N, c = i - r * a.N;  // 4 elements of one row (N % 4 == 0)
+      const int64_t row = 16 * s + r;
+      lanes::float4_t v = acc[t];
+      if (a.row_has_vector(row)) {
+        const lanes::float4_t vp = *reinterpret_cast<const lanes::float4_t*>(a.vpart + row * a.N + c);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = v[e] + vp[e];
+      }
+      T* dst = a.out + row * a.N + c;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) dst[e] = static_cast<T>(v[e]);
+    }
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(a.cnt + k0, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Work-groups [0, 8*per_xcd): window s (XCD-aware runs) computes its first
@@ -441,9 +533,9 @@ __global__ __launch_bounds__(64 * kMaxWaves) __attribute__((amdgpu_waves_per_eu(
       return;
     }
     const bool single = b1 - b0 <= a.kbig;
-    if (!single) b1 = b0 + a.kbig;
-    window_chunk<T, I, C, Loader>(a, s, b0, b1, single ? nullptr : a.slots + (2 * ((b0 + a.kbig) / a.kbig) + 1) * n16,
-                 s_col, s_val);
+    window_chunk<T, I, C, Loader>(a, s, b0, single ? b1 : b0 + a.kbig,
+                                  single ? nullptr : a.slots + (2 * ((b0 + a.kbig) / a.kbig) + 1) * n16, s_col, s_val);
+    if (!single) settle_window(a, s, b0, b1);
     return;
   }
   const int64_t k = g - lead;
@@ -456,61 +548,20 @@ __global__ __launch_bounds__(64 * kMaxWaves) __attribute__((amdgpu_waves_per_eu(
   const bool valid = s >= 0 && s < a.windows;
   const int64_t b0 = valid ? a.crp(s) : 0, b1 = valid ? a.crp(s + 1) : 0;
   const bool owns = valid && b0 < bk && b1 > b0 + a.kbig;
-  // Range k is the first overflow range of window s exactly when block bk
-  // lies in the window's second chunk; the combine pass starts there.
-  if (threadIdx.x == 0) a.first_of[k] = owns && (b0 + a.kbig) / a.kbig == k ? s : -1;
   if (!owns) return;
+  // Every overflow range from the window's second chunk, k0 = (b0 + kbig) /
+  // kbig, to (b1 - 1) / kbig holds a non-empty segment of it.
   const int64_t lo = b0 + a.kbig > bk ? b0 + a.kbig : bk;
   const int64_t hi = b1 < bk + a.kbig ? b1 : bk + a.kbig;
   if (lo >= hi) return;
   window_chunk<T, I, C, Loader>(a, s, lo, hi, a.slots + (2 * k) * n16, s_col, s_val);
+  settle_window(a, s, b0, b1);
 }
 
-// Combine pass, one work-group per (overflow range k, slice of 4*256 fp32
-// elements of the [16][N] window tile): if a window's blocks past its first
-// chunk start in range k (first_of[k]), each thread adds first chunk +
-// segments k, k+1, ... in order for its 4 elements, then adds the row's
-// vector sum where it has one, rounds once and writes the output.
-constexpr int kCombineThreads = 256;
-constexpr int kCombineSlice = 4 * kCombineThreads;
-template <typename T, typename I>
-__global__ __launch_bounds__(kCombineThreads) void block_combine(BlockArgs<T, I> a, int64_t slices) {
-  const int64_t k = static_cast<int64_t>(blockIdx.x) / slices;
-  const int64_t sl = static_cast<int64_t>(blockIdx.x) - k * slices;
-  const int64_t s = a.first_of[k];
-  if (s < 0) return;  // uniform over the work-group
-  const int64_t b1 = a.crp(s + 1);
-  const int64_t k_end = (b1 - 1) / a.kbig;
-  const int64_t n = 16 * a.N;
-  const int64_t i = sl * kCombineSlice + 4 * static_cast<int64_t>(threadIdx.x);
-  if (i >= n) return;
-  const lanes::float4_t* first = reinterpret_cast<const lanes::float4_t*>(a.slots + (2 * k + 1) * n + i);
-  lanes::float4_t acc = *first;
-  constexpr int kAhead = 8;
-  for (int64_t k0 = k; k0 <= k_end; k0 += kAhead) {
-    lanes::float4_t h[kAhead];
-#pragma unroll
-    for (int u = 0; u < kAhead; ++u) {
-      const int64_t kk = k0 + u <= k_end ? k0 + u : k_end;
-      h[u] = *reinterpret_cast<const lanes::float4_t*>(a.slots + (2 * kk) * n + i);
-    }
-#pragma unroll
-    for (int u = 0; u < kAhead; ++u)
-      if (k0 + u <= k_end) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) acc[e] = acc[e] + h[u][e];
-      }
-  }
-  const int64_t r = i / a.N, c = i - r * a.N;  // 4 elements of one row (N % 4 == 0)
-  const int64_t row = 16 * s + r;
-  if (a.row_has_vector(row)) {
-    const lanes::float4_t vp = *reinterpret_cast<const lanes::float4_t*>(a.vpart + row * a.N + c);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) acc[e] = acc[e] + vp[e];
-  }
-  T* dst = a.out + row * a.N + c;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) dst[e] = static_cast<T>(acc[e]);
+// Zeroes the window counters when no earlier kernel of the call did.
+__global__ __launch_bounds__(256) void block_zero_counts(uint32_t* cnt, int64_t n) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) cnt[i] = 0u;
 }
 
 template <typename T, typename I>
@@ -518,7 +569,7 @@ spmm_status block_typed(const void* Crowptr, const void* Ccol, const void* Cvalu
                         int64_t block_count, int64_t block_values, const void* Vrowptr,
                         int64_t vector_rows, int64_t vector_nnz, const void* dense, int64_t K,
                         int64_t N, void* out, const float* vpart, float* slots, const int32_t* order,
-                        hipStream_t stream) {
+                        bool zero_counts, hipStream_t stream) {
   if (windows <= 0) return SPMM_OK;
   if (K > static_cast<int64_t>(kBadCol) - 1)
     return fail(SPMM_ERR_CONTRACT, "dense has too many rows for 32-bit column ids");
@@ -542,7 +593,7 @@ spmm_status block_typed(const void* Crowptr, const void* Ccol, const void* Cvalu
   a.order = order;
   a.kbig = block_chunk_for(sizeof(T) == 2 ? SPMM_VALUE_F16 : SPMM_VALUE_F32, a.limit);
   a.noverflow = block_overflow_ranges(a.limit, a.kbig);
-  a.first_of = reinterpret_cast<int64_t*>(slots + a.noverflow * 2 * 16 * N);
+  a.cnt = reinterpret_cast<uint32_t*>(slots + a.noverflow * 2 * 16 * N);
   a.per_xcd = ceil_div(windows, kXcds * kBlockXcdRun) * kBlockXcdRun;
   const int C = lane_cols_for<T>(N);
   const int64_t groups = ceil_div(N, 16 * C);
@@ -563,13 +614,13 @@ spmm_status block_typed(const void* Crowptr, const void* Ccol, const void* Cvalu
                                  : block_windows<T, I, 4, BlockBufferLoader<T, 4>>)
                        : (C == 8 ? block_windows<T, I, kWide, BlockGlobalLoader<T, kWide>>
                                  : block_windows<T, I, 4, BlockGlobalLoader<T, 4>>);
+  if (zero_counts && a.noverflow > 0) {
+    hipLaunchKernelGGL(block_zero_counts, dim3(static_cast<unsigned>(ceil_div(a.noverflow, 256))), dim3(256), 0,
+                       stream, a.cnt, a.noverflow);
+    if (spmm_status st = check_launch("block_zero_counts")) return st;
+  }
   hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(grid)), dim3(64 * waves), stage_lds, stream, a);
-  if (spmm_status st = check_launch("block_windows")) return st;
-  if (a.noverflow == 0) return SPMM_OK;
-  const int64_t slices = ceil_div(16 * N, kCombineSlice);
-  hipLaunchKernelGGL((block_combine<T, I>), dim3(static_cast<unsigned>(a.noverflow * slices)),
-                     dim3(kCombineThreads), 0, stream, a, slices);
-  return check_launch("block_combine");
+  return check_launch("block_windows");
 }
 
 }  // namespace
@@ -583,11 +634,11 @@ spmm_status launch_block(int32_t index_type, int32_t value_type, const void* Cro
                          int64_t block_count, int64_t block_values, const void* Vrowptr,
                          int64_t vector_rows, int64_t vector_nnz, const void* dense,
                          int64_t dense_rows, int64_t width, void* out, const float* vpart,
-                         float* slots, const int32_t* order, hipStream_t stream) {
+                         float* slots, const int32_t* order, bool zero_counts, hipStream_t stream) {
 #define SPMM_BLOCK_CALL(T, I)                                                                   \
   return block_typed<T, I>(Crowptr, Ccol, Cvalue, windows, block_count, block_values, Vrowptr, \
                            vector_rows, vector_nnz, dense, dense_rows, width, out, vpart, slots, \
-                           order, stream)
+                           order, zero_counts, stream)
   if (value_type == SPMM_VALUE_F16) {
     if (index_type == SPMM_INDEX_I32) SPMM_BLOCK_CALL(_Float16, int32_t);
     SPMM_BLOCK_CALL(_Float16, int64_t);

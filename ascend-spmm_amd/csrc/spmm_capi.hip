@@ -143,7 +143,7 @@ spmm_status spmm_csr_run(const spmm_csr_desc* d, const void* rowptr, const void*
   if (spmm_status st = check_csr_pointers(d, rowptr, col, value, dense, out, "spmm_csr")) return st;
   return launch_gather(d->index_type, d->value_type, rowptr, col, value, d->nnz, d->rows, 0, d->rows,
                        dense, d->dense_rows, d->width, out, workspace, workspace_bytes, nullptr, 0, 0,
-                       nullptr, nullptr, nullptr, as_stream(stream));
+                       nullptr, nullptr, nullptr, nullptr, 0, as_stream(stream));
 }
 
 size_t spmm_csr_noalloc_max_scratch(void) { return kNoallocScratchBytes; }
@@ -168,7 +168,7 @@ spmm_status spmm_csr_run_noalloc(const spmm_csr_desc* d, const void* rowptr, con
   // and each partial slot before the post pass reads it.
   return launch_gather(d->index_type, d->value_type, rowptr, col, value, d->nnz, d->rows, 0, d->rows,
                        dense, d->dense_rows, d->width, out, ws, kNoallocScratchBytes, nullptr, 0, 0,
-                       nullptr, nullptr, nullptr, as_stream(stream));
+                       nullptr, nullptr, nullptr, nullptr, 0, as_stream(stream));
 }
 
 spmm_status spmm_csr_rowscalar_run(const spmm_csr_desc* d, const void* rowptr, const void* col,
@@ -200,11 +200,11 @@ int64_t spmm_mixed_out_rows(const spmm_mixed_desc* d) {
 namespace {
 // Workspace of the mixed operator: gather part, then the fp32 vector sums of
 // block-window rows ([16*windows][width]), then the pieces of windows longer
-// than the block chunk ([ranges][2][16][width]) and the window starting in
-// each overflow range ([ranges] int64).
+// than the block chunk ([ranges][2][16][width]) and one counter per overflow
+// range ([ranges] uint32, zeroed by the call before the block kernel).
 struct MixedLayout {
   size_t gather = 0, vpart = 0, slots = 0, order = 0;
-  int64_t limit = 0;
+  int64_t limit = 0, ranges = 0;
   explicit MixedLayout(const spmm_mixed_desc* d) {
     const int64_t w = d->width > 0 ? d->width : 0;
     gather = align_up(gather_workspace_bytes(d->vector_nnz < 0 ? 0 : d->vector_nnz, w), 256);
@@ -214,9 +214,9 @@ struct MixedLayout {
     vpart = align_up(static_cast<size_t>(16 * windows) * w * sizeof(float), 256);
     limit = d->block_count < d->block_values / 16 ? d->block_count : d->block_values / 16;
     if (limit < 0) limit = 0;
-    const int64_t ranges = block_overflow_ranges(limit, block_chunk_for(d->value_type, limit));
+    ranges = block_overflow_ranges(limit, block_chunk_for(d->value_type, limit));
     slots = align_up(static_cast<size_t>(ranges * 2 * 16) * w * sizeof(float) +
-                         static_cast<size_t>(ranges) * sizeof(int64_t), 256);
+                         static_cast<size_t>(ranges) * sizeof(uint32_t), 256);
     // The block windows' locality order (block_order_wanted).
     order = block_order_wanted(d->block_windows, d->vector_nnz, w, d->value_type)
                 ? align_up(static_cast<size_t>(d->block_windows) * sizeof(int32_t), 256)
@@ -271,15 +271,20 @@ spmm_status spmm_mixed_run(const spmm_mixed_desc* d, const void* Crowptr, const 
   // blocks itself, and the vector pass only covers rows past the windows.
   // With the window order (block_order_wanted), the vector pass's kernel also
   // writes the block windows' locality order, which the block kernel follows.
+  // The block kernel's window counters (after the pieces in `slots`) start
+  // at zero: the gather's post pass zeroes them when it runs (it always does
+  // when the gather covers any row), else the block launch does.
   const int64_t row_lo = d->vector_nnz == 0 ? 16 * d->block_windows : 0;
+  const bool gather_runs = out_rows > row_lo;
+  uint32_t* counts = reinterpret_cast<uint32_t*>(slots + lay.ranges * 2 * 16 * d->width);
   spmm_status st = launch_gather(d->index_type, d->value_type, Vrowptr, Vcol, Vvalue, d->vector_nnz,
                                  d->vector_rows, row_lo, out_rows, dense, d->dense_rows, d->width, out, ws,
                                  lay.gather, d->block_windows > 0 ? Crowptr : nullptr, d->block_windows,
-                                 lay.limit, vpart, Ccol, order, s);
+                                 lay.limit, vpart, Ccol, order, lay.ranges > 0 ? counts : nullptr, lay.ranges, s);
   if (st != SPMM_OK) return st;
   return launch_block(d->index_type, d->value_type, Crowptr, Ccol, Cvalue, d->block_windows,
                       d->block_count, d->block_values, Vrowptr, d->vector_rows, d->vector_nnz, dense,
-                      d->dense_rows, d->width, out, vpart, slots, order, s);
+                      d->dense_rows, d->width, out, vpart, slots, order, !gather_runs, s);
 }
 
 }  // extern "C"

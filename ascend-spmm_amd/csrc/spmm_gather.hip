@@ -646,13 +646,21 @@ __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM
 // Post pass, one launch:
 //  * work-groups [0, fix_blocks): add the partials of every row that crosses
 //    range ends, in range order (lane group per (range, column chunk));
+//  * the next zero_blocks: zero the block kernel's window counters (mixed
+//    operator), which that kernel expects at zero;
 //  * the rest: empty rows, 64 per wavefront, are written as zeros (rows of
 //    block windows with blocks are left to the block kernel).
 template <typename T, typename I>
 __global__ __launch_bounds__(kWgThreads) void gather_post(Geometry<I> g, int64_t N, T* __restrict__ out,
                                                           const float* __restrict__ ws, int log2L,
-                                                          int64_t chunks, int64_t slot, int64_t fix_blocks) {
+                                                          int64_t chunks, int64_t slot, int64_t fix_blocks,
+                                                          uint32_t* zero_counts, int64_t count, int64_t zero_blocks) {
   constexpr int V = LaneVec<T>::V;
+  if (static_cast<int64_t>(blockIdx.x) >= fix_blocks && static_cast<int64_t>(blockIdx.x) < fix_blocks + zero_blocks) {
+    const int64_t i = (static_cast<int64_t>(blockIdx.x) - fix_blocks) * blockDim.x + threadIdx.x;
+    if (i < count) zero_counts[i] = 0u;
+    return;
+  }
   if (static_cast<int64_t>(blockIdx.x) < fix_blocks) {
     const int L = 1 << log2L;
     const int64_t tid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -707,7 +715,8 @@ __global__ __launch_bounds__(kWgThreads) void gather_post(Geometry<I> g, int64_t
   }
   // Empty rows: wavefront w takes rows [row_lo + 64w, +64).
   const int lane = threadIdx.x & 63;
-  const int64_t wave = (static_cast<int64_t>(blockIdx.x) - fix_blocks) * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int64_t wave =
+      (static_cast<int64_t>(blockIdx.x) - fix_blocks - zero_blocks) * (blockDim.x >> 6) + (threadIdx.x >> 6);
   const int64_t r = g.row_lo + wave * 64 + lane;
   // Rows of block windows with blocks are written by the block kernel.
   const bool zero_row = r < g.row_hi && g.rp(r) == g.rp(r + 1) && !g.in_block_window(r);
@@ -730,7 +739,7 @@ spmm_status gather_typed(const void* rowptr, const void* col, const void* value,
                          int64_t vrows, int64_t row_lo, int64_t row_hi, const void* dense, int64_t K,
                          int64_t N, void* out, void* ws, size_t ws_bytes, const void* Crowptr,
                          int64_t cwin, int64_t climit, float* vpart, const void* Ccol, int32_t* order,
-                         hipStream_t stream) {
+                         uint32_t* zero_counts, int64_t count, hipStream_t stream) {
   constexpr int V = LaneVec<T>::V;
   if (row_hi <= row_lo) return SPMM_OK;
   Geometry<I> g;
@@ -808,9 +817,11 @@ spmm_status gather_typed(const void* rowptr, const void* col, const void* value,
   const int64_t fix_items = g.nnz > 0 ? (g.nranges - 1) * chunks * L : 0;
   const int64_t fix_blocks = ceil_div(fix_items, kWgThreads);
   const int64_t row_blocks = ceil_div(ceil_div(row_hi - row_lo, 64), kWgThreads / 64);
-  hipLaunchKernelGGL((gather_post<T, I>), dim3(static_cast<unsigned>(fix_blocks + row_blocks)),
+  const int64_t zero_blocks = zero_counts != nullptr ? ceil_div(count, kWgThreads) : 0;
+  hipLaunchKernelGGL((gather_post<T, I>), dim3(static_cast<unsigned>(fix_blocks + zero_blocks + row_blocks)),
                      dim3(kWgThreads), 0, stream, g, N, static_cast<T*>(out),
-                     static_cast<const float*>(partial), log2L, chunks, slot, fix_blocks);
+                     static_cast<const float*>(partial), log2L, chunks, slot, fix_blocks, zero_counts, count,
+                     zero_blocks);
   return check_launch("gather_post");
 }
 
@@ -827,11 +838,12 @@ spmm_status launch_gather(int32_t index_type, int32_t value_type, const void* ro
                           int64_t row_lo, int64_t row_hi, const void* dense, int64_t dense_rows,
                           int64_t width, void* out, void* workspace, size_t workspace_bytes,
                           const void* Crowptr, int64_t cwin, int64_t climit, float* vpart,
-                          const void* Ccol, int32_t* order, hipStream_t stream) {
+                          const void* Ccol, int32_t* order, uint32_t* zero_counts, int64_t count,
+                          hipStream_t stream) {
 #define SPMM_GATHER_CALL(T, I)                                                                 \
   return gather_typed<T, I>(rowptr, col, value, nnz, vrows, row_lo, row_hi, dense, dense_rows, \
                             width, out, workspace, workspace_bytes, Crowptr, cwin, climit, vpart, \
-                            Ccol, order, stream)
+                            Ccol, order, zero_counts, count, stream)
   if (value_type == SPMM_VALUE_F16) {
     if (index_type == SPMM_INDEX_I32) SPMM_GATHER_CALL(_Float16, int32_t);
     SPMM_GATHER_CALL(_Float16, int64_t);

@@ -61,10 +61,10 @@ MFMA_PEAK_TFLOPS = {"fp16": 2500.0, "fp32": 157.3}
 OP_KERNELS = {
     "csr": "gather_tiles + gather_post (one spmm_csr call)",
     "mixed-empty": "gather_tiles + gather_post (spmm_ascend_cube, empty block part)",
-    "bcsr": "block_windows (+ block_combine when overflow ranges exist)",
-    "mixed": "gather_tiles + gather_post + block_windows (+ block_combine)",
+    "bcsr": "block_windows (+ block_zero_counts when windows can overflow)",
+    "mixed": "gather_tiles + gather_post + block_windows",
     "graph": ("fill_minus_one + scatter_inverse + gather_rows (pack) + gather_tiles + gather_post + "
-              "block_windows + block_combine + gather_rows (restore)"),
+              "block_windows + gather_rows (restore)"),
 }
 FETCH_SCALE = 2.0
 WRITE_SCALE = 1.0
