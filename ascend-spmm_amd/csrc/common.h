@@ -35,6 +35,28 @@ constexpr int kXcds = 8;
 
 inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
+// Bytes a raw buffer resource must span to read `width` columns of each of K
+// rows that lie ld elements apart: the last row's slab ends there.
+__host__ __device__ inline int64_t buffer_extent(int64_t K, int64_t ld, int64_t width, int64_t elem_bytes) {
+  return K > 0 ? ((K - 1) * ld + width) * elem_bytes : 0;
+}
+
+// Column passes.  A dense operand much larger than the 256 MB Infinity Cache
+// is swept in slabs of `pass_width` columns (rows ld = N apart), one SpMM
+// pass per slab: the gathers of a pass then hit a 512 MiB slab instead of the
+// whole operand.  Every output element is computed by the same operation
+// sequence as in one full-width pass (the kernels' results do not depend on
+// the width), so the passes change only the speed: config 5 (1M x 512 fp32,
+// 2 GiB) takes 10.4 ms in four passes of 128 columns against 12.3 ms in one.
+// Slabs keep at least 512-byte rows (narrower ones were slower there).
+constexpr int64_t kPassSlabBytes = int64_t(512) << 20;
+constexpr int64_t kPassMinRowBytes = 512;
+inline int64_t pass_width(int64_t K, int64_t N, int64_t elem_bytes) {
+  int64_t w = N;
+  while (w % 32 == 0 && (w / 2) * elem_bytes >= kPassMinRowBytes && K * w * elem_bytes > kPassSlabBytes) w /= 2;
+  return w;
+}
+
 // Split length R of the CSR gather path: nonzero positions are cut into
 // ranges [j*R, (j+1)*R), one lane group per range.  R is the largest power of
 // two in [kGatherRangeMin, kGatherRangeMax] with about nnz / R >=
@@ -65,12 +87,14 @@ inline int64_t gather_slot_floats(int64_t width) { return (width + 63) / 64 * 64
 // With a block part (Crowptr != nullptr, cwin windows, climit usable blocks),
 // the vector sums of rows in block windows with blocks go to `vpart` (fp32)
 // instead of `out`, and their empty rows are left to the block kernel.
-// `zero_counts` (count entries, may be null) is zeroed by the post pass, for
-// the block kernel that runs next.
+// `dense` and `out` hold `width` columns per row, rows `ld` elements apart
+// (ld >= width: a column slab of wider matrices); vpart rows hold `width`
+// floats.  `zero_counts` (count entries, may be null) is zeroed by the post
+// pass, for the block kernel that runs next.
 spmm_status launch_gather(int32_t index_type, int32_t value_type,
                           const void* rowptr, const void* col, const void* value,
                           int64_t nnz, int64_t vrows, int64_t row_lo, int64_t row_hi,
-                          const void* dense, int64_t dense_rows, int64_t width,
+                          const void* dense, int64_t dense_rows, int64_t width, int64_t ld,
                           void* out, void* workspace, size_t workspace_bytes,
                           const void* Crowptr, int64_t cwin, int64_t climit, float* vpart,
                           const void* Ccol, int32_t* order, uint32_t* zero_counts, int64_t count,
@@ -117,7 +141,9 @@ inline int64_t block_chunk_for(int32_t value_type, int64_t blocks) {
 // Number of fixed overflow ranges for `blocks` usable blocks.
 int64_t block_overflow_ranges(int64_t blocks, int64_t kbig);
 
-// Block (BCSR 16x1) part.  Runs after the gather pass: every window with
+// Block (BCSR 16x1) part.  `dense` and `out` rows are `ld` elements apart,
+// `width` columns computed (vpart and slots rows hold `width` floats).  Runs
+// after the gather pass: every window with
 // blocks is written to `out` as block sum + the fp32 vector sums the gather
 // pass left in `vpart` ([16*windows][width]) for its rows with vector
 // nonzeros, rounded once.  `slots` holds the pieces of windows longer than
@@ -129,7 +155,7 @@ spmm_status launch_block(int32_t index_type, int32_t value_type,
                          const void* Crowptr, const void* Ccol, const void* Cvalue,
                          int64_t windows, int64_t block_count, int64_t block_values,
                          const void* Vrowptr, int64_t vector_rows, int64_t vector_nnz,
-                         const void* dense, int64_t dense_rows, int64_t width,
+                         const void* dense, int64_t dense_rows, int64_t width, int64_t ld,
                          void* out, const float* vpart, float* slots, const int32_t* order,
                          bool zero_counts, hipStream_t stream);
 

@@ -97,7 +97,7 @@ struct BlockArgs {
   const I* Vrowptr;
   int64_t vrows, vnnz;     // vector part: rows and nonzeros
   const T* dense;
-  int64_t K, N;
+  int64_t K, N, ld;        // N columns computed; dense and out rows are ld elements apart
   T* out;
   const float* vpart;      // [16*windows][N] fp32 vector sums of block-window rows (gather pass)
   float* slots;            // [noverflow][2][16][N] fp32 partials of windows longer than kbig
@@ -156,17 +156,17 @@ struct BlockBufferLoader {
   spmm_block_rsrc_t rsrc;
   uint32_t lane_bytes;
   static constexpr uint32_t kNone = kBlockBufferNone;
-  __device__ inline BlockBufferLoader(const T* dense, int64_t K, int64_t N, int64_t col0) {
+  __device__ inline BlockBufferLoader(const T* dense, int64_t K, int64_t ld, int64_t N, int64_t col0) {
     const uint64_t p = reinterpret_cast<uint64_t>(dense);
     rsrc[0] = static_cast<int>(p & 0xFFFFFFFFu);
     rsrc[1] = static_cast<int>((p >> 32) & 0xFFFFu);  // stride 0: raw buffer
-    rsrc[2] = static_cast<int>(static_cast<uint32_t>(K * N * static_cast<int64_t>(sizeof(T))));
+    rsrc[2] = static_cast<int>(static_cast<uint32_t>(buffer_extent(K, ld, N, sizeof(T))));
     rsrc[3] = 0x00020000;  // 32-bit data format; no swizzle, no thread-id offset
     lane_bytes = static_cast<uint32_t>(col0 * static_cast<int64_t>(sizeof(T)));
   }
-  __device__ static inline uint32_t stage(int64_t c, int64_t K, int64_t N) {
+  __device__ static inline uint32_t stage(int64_t c, int64_t K, int64_t ld) {
     return static_cast<uint64_t>(c) < static_cast<uint64_t>(K)
-               ? static_cast<uint32_t>(c) * static_cast<uint32_t>(N * static_cast<int64_t>(sizeof(T)))
+               ? static_cast<uint32_t>(c) * static_cast<uint32_t>(ld * static_cast<int64_t>(sizeof(T)))
                : kNone;
   }
   __device__ inline Piece<T, C> load(uint32_t src) const {
@@ -184,16 +184,16 @@ constexpr uint32_t kBadCol = 0xFFFFFFFFu;
 template <typename T, int C>
 struct BlockGlobalLoader {
   const T* dense_c;  // dense + the lane's first column
-  uint32_t N;
+  uint32_t ld;  // row stride of dense (elements)
   static constexpr uint32_t kNone = kBadCol;
-  __device__ inline BlockGlobalLoader(const T* dense, int64_t, int64_t n, int64_t col0)
-      : dense_c(dense + col0), N(static_cast<uint32_t>(n)) {}
+  __device__ inline BlockGlobalLoader(const T* dense, int64_t, int64_t ld_, int64_t, int64_t col0)
+      : dense_c(dense + col0), ld(static_cast<uint32_t>(ld_)) {}
   __device__ static inline uint32_t stage(int64_t c, int64_t K, int64_t) {
     return static_cast<uint64_t>(c) < static_cast<uint64_t>(K) ? static_cast<uint32_t>(c) : kNone;
   }
   __device__ inline Piece<T, C> load(uint32_t src) const {
     const bool ok = src != kNone;
-    const Piece<T, C> x = *reinterpret_cast<const Piece<T, C>*>(dense_c + static_cast<uint64_t>(ok ? src : 0u) * N);
+    const Piece<T, C> x = *reinterpret_cast<const Piece<T, C>*>(dense_c + static_cast<uint64_t>(ok ? src : 0u) * ld);
     return ok ? x : Piece<T, C>(static_cast<T>(0));
   }
 };
@@ -206,7 +206,15 @@ struct BlockGlobalLoader {
 // checks.  With `finish` set it also returns the window's vector-row bits
 // (bit r: row 16*s + r has vector-part nonzeros, whose fp32 sum is in vpart),
 // read in the same round trip.
-template <typename T, typename I, typename Loader>
+// Row stride of dense and out: a.ld for a column pass of a wider operand
+// (kS), else the width itself.  A compile-time choice: the one-pass kernels
+// keep the offsets (and registers) of a stride equal to the width.
+template <bool kS, typename T, typename I>
+__device__ inline int64_t row_stride(const BlockArgs<T, I>& a) {
+  return kS ? a.ld : a.N;
+}
+
+template <typename T, typename I, typename Loader, bool kS>
 __device__ inline unsigned stage_chunk(const BlockArgs<T, I>& a, int64_t s, bool finish, int64_t b0,
                                        int64_t b1, uint32_t* s_src, T* s_val) {
   __shared__ unsigned s_vec;
@@ -215,7 +223,7 @@ __device__ inline unsigned stage_chunk(const BlockArgs<T, I>& a, int64_t s, bool
   if (threadIdx.x == 0) s_vec = 0;
   const bool vec = finish && threadIdx.x < 16 && a.row_has_vector(16 * s + threadIdx.x);
   for (int64_t i = threadIdx.x; i < n_pad; i += blockDim.x)
-    s_src[i] = i < n ? Loader::stage(static_cast<int64_t>(a.Ccol[b0 + i]), a.K, a.N) : Loader::kNone;
+    s_src[i] = i < n ? Loader::stage(static_cast<int64_t>(a.Ccol[b0 + i]), a.K, row_stride<kS>(a)) : Loader::kNone;
   constexpr int64_t kPer = 16 * sizeof(T) / 16;  // 16-byte pieces per block
   const lanes::raw16_t* src = reinterpret_cast<const lanes::raw16_t*>(a.Cvalue + 16 * b0);
   lanes::raw16_t* dst = reinterpret_cast<lanes::raw16_t*>(s_val);
@@ -255,13 +263,13 @@ struct StepOperands {
 // holds C consecutive output columns of rows 4kg .. 4kg+3.  With C = 4 the
 // loads of the next K-step are issued before the current step's MFMAs (two
 // steps of operands in registers).  Adds to `acc`.
-template <typename T, typename I, int C, typename Loader>
+template <typename T, typename I, int C, typename Loader, bool kS>
 __device__ inline void group_sum(const BlockArgs<T, I>& a, const uint32_t* s_src, const T* s_val,
                                  int64_t n, int64_t n0, int lane, float4_t (&acc)[C]) {
   static_assert(C == 4 || (C == 8 && sizeof(T) == 2), "lane columns: 4, or 8 for fp16");
   const int q = lane & 15, kg = lane >> 4;
   const int64_t col0 = n0 + C * q < a.N ? n0 + C * q : 0;  // N % C == 0
-  const Loader ld(a.dense, a.K, a.N, col0);
+  const Loader ld(a.dense, a.K, row_stride<kS>(a), a.N, col0);
   if (a.K <= 0 || n <= 0) return;  // uniform: no valid dense row
   const int32_t steps = static_cast<int32_t>((n + k_step<T>() - 1) / k_step<T>());
 
@@ -340,18 +348,18 @@ __device__ inline unsigned window_vector_rows(const BlockArgs<T, I>& a, int64_t 
 // sum goes to that [16][N] workspace slot instead.  Blocks are staged in LDS
 // `a.stage` at a time (a multiple of the K-step, so the MFMA sequence does
 // not depend on it); a window that fits is staged once for all column groups.
-template <typename T, typename I, int C, typename Loader>
+template <typename T, typename I, int C, typename Loader, bool kS>
 __device__ inline void window_chunk(const BlockArgs<T, I>& a, int64_t s, int64_t b0, int64_t b1,
                                     float* slot, uint32_t* s_col, T* s_val) {
   const int64_t n = b1 - b0;
   const bool once = n <= a.stage;
   unsigned vec = 0;
   if (once)
-    vec = stage_chunk<T, I, Loader>(a, s, slot == nullptr, b0, b1, s_col, s_val);
+    vec = stage_chunk<T, I, Loader, kS>(a, s, slot == nullptr, b0, b1, s_col, s_val);
   else if (slot == nullptr)
     vec = window_vector_rows(a, s);
   constexpr int64_t kGroupCols = 16 * C;
-  T* const out_w = a.out + 16 * s * a.N;
+  T* const out_w = a.out + 16 * s * row_stride<kS>(a);
   const float* const vpart_w = a.vpart + 16 * s * a.N;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int waves = blockDim.x >> 6;
@@ -366,13 +374,13 @@ __device__ inline void window_chunk(const BlockArgs<T, I>& a, int64_t s, int64_t
 #pragma unroll
     for (int j = 0; j < C; ++j) acc[j] = float4_t{0.f, 0.f, 0.f, 0.f};
     if (once) {
-      if (active) group_sum<T, I, C, Loader>(a, s_col, s_val, n, n0, lane, acc);
+      if (active) group_sum<T, I, C, Loader, kS>(a, s_col, s_val, n, n0, lane, acc);
     } else {
       for (int64_t sb = 0; sb < n; sb += a.stage) {
         const int64_t m = n - sb < a.stage ? n - sb : a.stage;
         __syncthreads();  // the previous piece is no longer read
-        stage_chunk<T, I, Loader>(a, s, false, b0 + sb, b0 + sb + m, s_col, s_val);
-        if (active) group_sum<T, I, C, Loader>(a, s_col, s_val, m, n0, lane, acc);
+        stage_chunk<T, I, Loader, kS>(a, s, false, b0 + sb, b0 + sb + m, s_col, s_val);
+        if (active) group_sum<T, I, C, Loader, kS>(a, s_col, s_val, m, n0, lane, acc);
       }
     }
     const int64_t c0 = n0 + C * q;
@@ -383,7 +391,8 @@ __device__ inline void window_chunk(const BlockArgs<T, I>& a, int64_t s, int64_t
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int r = 4 * kg + e;
-      const uint32_t o = static_cast<uint32_t>(r * a.N + c0);
+      const uint32_t o = static_cast<uint32_t>(r * a.N + c0);  // in the [16][N] vpart / slot tile
+      const uint32_t oo = kS ? static_cast<uint32_t>(r * a.ld + c0) : o;  // in the output window
       float v[C];
 #pragma unroll
       for (int j = 0; j < C; ++j) v[j] = acc[j][e];
@@ -407,7 +416,7 @@ __device__ inline void window_chunk(const BlockArgs<T, I>& a, int64_t s, int64_t
           for (int i = 0; i < 4; ++i) v[w + i] = v[w + i] + p[i];
         }
       }
-      store_cols<T, C>(out_w + o, v);
+      store_cols<T, C>(out_w + oo, v);
     }
   }
 }
@@ -419,7 +428,7 @@ __device__ inline void window_chunk(const BlockArgs<T, I>& a, int64_t s, int64_t
 // count adds first chunk + segments k0, k0+1, ... in order, adds the rows'
 // vector sums, rounds once and writes the window's 16 rows, then resets the
 // counter to zero for the next call.  All threads of the work-group call it.
-template <typename T, typename I>
+template <bool kS, typename T, typename I>
 __device__ inline void settle_window(const BlockArgs<T, I>& a, int64_t s, int64_t b0, int64_t b1) {
   __shared__ uint32_t s_last;
   const int64_t k0 = (b0 + a.kbig) / a.kbig;
@@ -487,7 +496,7 @@ __device__ inline void settle_window(const BlockArgs<T, I>& a, int64_t s, int64_
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] = v[e] + vp[e];
       }
-      T* dst = a.out + row * a.N + c;
+      T* dst = a.out + row * row_stride<kS>(a) + c;
 #pragma unroll
       for (int e = 0; e < 4; ++e) dst[e] = static_cast<T>(v[e]);
     }
@@ -509,7 +518,7 @@ __device__ inline void settle_window(const BlockArgs<T, I>& a, int64_t s, int64_
 #endif
 // Waves per SIMD the register budget of block_windows is fitted to (C = 8
 // holds twice the accumulators and dense pieces).
-template <typename T, typename I, int C, typename Loader>
+template <typename T, typename I, int C, typename Loader, bool kS>
 __global__ __launch_bounds__(64 * kMaxWaves) __attribute__((amdgpu_waves_per_eu(C == 8 ? SPMM_BLOCK_WAVES_WIDE : SPMM_BLOCK_WAVES))) void block_windows(BlockArgs<T, I> a) {
   extern __shared__ __align__(16) unsigned char smem[];
   T* s_val = reinterpret_cast<T*>(smem);                           // [stage][16]
@@ -526,16 +535,19 @@ __global__ __launch_bounds__(64 * kMaxWaves) __attribute__((amdgpu_waves_per_eu(
     int64_t b1 = a.crp(s + 1);
     if (b1 <= b0) {  // empty window: its rows are the vector pass's, or zeros
       if (a.zero_empty) {
-        lanes::raw16_t* dst = reinterpret_cast<lanes::raw16_t*>(a.out + 16 * s * a.N);
-        const int64_t pieces = n16 * static_cast<int64_t>(sizeof(T)) / 16;
-        for (int64_t i = threadIdx.x; i < pieces; i += blockDim.x) dst[i] = lanes::raw16_t{0u, 0u, 0u, 0u};
+        const int64_t per_row = a.N * static_cast<int64_t>(sizeof(T)) / 16;  // 16-byte pieces of a row
+        for (int64_t i = threadIdx.x; i < 16 * per_row; i += blockDim.x) {
+          const int64_t r = i / per_row;
+          reinterpret_cast<lanes::raw16_t*>(a.out + (16 * s + r) * row_stride<kS>(a))[i - r * per_row] =
+              lanes::raw16_t{0u, 0u, 0u, 0u};
+        }
       }
       return;
     }
     const bool single = b1 - b0 <= a.kbig;
-    window_chunk<T, I, C, Loader>(a, s, b0, single ? b1 : b0 + a.kbig,
+    window_chunk<T, I, C, Loader, kS>(a, s, b0, single ? b1 : b0 + a.kbig,
                                   single ? nullptr : a.slots + (2 * ((b0 + a.kbig) / a.kbig) + 1) * n16, s_col, s_val);
-    if (!single) settle_window(a, s, b0, b1);
+    if (!single) settle_window<kS>(a, s, b0, b1);
     return;
   }
   const int64_t k = g - lead;
@@ -554,8 +566,8 @@ __global__ __launch_bounds__(64 * kMaxWaves) __attribute__((amdgpu_waves_per_eu(
   const int64_t lo = b0 + a.kbig > bk ? b0 + a.kbig : bk;
   const int64_t hi = b1 < bk + a.kbig ? b1 : bk + a.kbig;
   if (lo >= hi) return;
-  window_chunk<T, I, C, Loader>(a, s, lo, hi, a.slots + (2 * k) * n16, s_col, s_val);
-  settle_window(a, s, b0, b1);
+  window_chunk<T, I, C, Loader, kS>(a, s, lo, hi, a.slots + (2 * k) * n16, s_col, s_val);
+  settle_window<kS>(a, s, b0, b1);
 }
 
 // Zeroes the window counters when no earlier kernel of the call did.
@@ -568,7 +580,7 @@ template <typename T, typename I>
 spmm_status block_typed(const void* Crowptr, const void* Ccol, const void* Cvalue, int64_t windows,
                         int64_t block_count, int64_t block_values, const void* Vrowptr,
                         int64_t vector_rows, int64_t vector_nnz, const void* dense, int64_t K,
-                        int64_t N, void* out, const float* vpart, float* slots, const int32_t* order,
+                        int64_t N, int64_t ldd, void* out, const float* vpart, float* slots, const int32_t* order,
                         bool zero_counts, hipStream_t stream) {
   if (windows <= 0) return SPMM_OK;
   if (K > static_cast<int64_t>(kBadCol) - 1)
@@ -586,6 +598,7 @@ spmm_status block_typed(const void* Crowptr, const void* Ccol, const void* Cvalu
   a.dense = static_cast<const T*>(dense);
   a.K = K;
   a.N = N;
+  a.ld = ldd;
   a.out = static_cast<T*>(out);
   a.vpart = vpart;
   a.slots = slots;
@@ -609,11 +622,16 @@ spmm_status block_typed(const void* Crowptr, const void* Ccol, const void* Cvalu
   const int64_t grid = a.per_xcd * kXcds + a.noverflow;
   constexpr int kWide = sizeof(T) == 2 ? 8 : 4;  // fp32 only has C = 4
   // Dense operands within a 32-bit byte extent use buffer loads.
-  const bool buffer = K * N * static_cast<int64_t>(sizeof(T)) <= kBlockBufferLimit;
-  auto kernel = buffer ? (C == 8 ? block_windows<T, I, kWide, BlockBufferLoader<T, kWide>>
-                                 : block_windows<T, I, 4, BlockBufferLoader<T, 4>>)
-                       : (C == 8 ? block_windows<T, I, kWide, BlockGlobalLoader<T, kWide>>
-                                 : block_windows<T, I, 4, BlockGlobalLoader<T, 4>>);
+  const bool buffer = buffer_extent(K, ldd, N, sizeof(T)) <= kBlockBufferLimit;
+  // Column passes (ldd > N) take the strided instantiations.
+  auto kernel = ldd == N ? (buffer ? (C == 8 ? block_windows<T, I, kWide, BlockBufferLoader<T, kWide>, false>
+                                            : block_windows<T, I, 4, BlockBufferLoader<T, 4>, false>)
+                                   : (C == 8 ? block_windows<T, I, kWide, BlockGlobalLoader<T, kWide>, false>
+                                             : block_windows<T, I, 4, BlockGlobalLoader<T, 4>, false>))
+                         : (buffer ? (C == 8 ? block_windows<T, I, kWide, BlockBufferLoader<T, kWide>, true>
+                                            : block_windows<T, I, 4, BlockBufferLoader<T, 4>, true>)
+                                   : (C == 8 ? block_windows<T, I, kWide, BlockGlobalLoader<T, kWide>, true>
+                                             : block_windows<T, I, 4, BlockGlobalLoader<T, 4>, true>));
   if (zero_counts && a.noverflow > 0) {
     hipLaunchKernelGGL(block_zero_counts, dim3(static_cast<unsigned>(ceil_div(a.noverflow, 256))), dim3(256), 0,
                        stream, a.cnt, a.noverflow);
@@ -633,11 +651,11 @@ spmm_status launch_block(int32_t index_type, int32_t value_type, const void* Cro
                          const void* Ccol, const void* Cvalue, int64_t windows,
                          int64_t block_count, int64_t block_values, const void* Vrowptr,
                          int64_t vector_rows, int64_t vector_nnz, const void* dense,
-                         int64_t dense_rows, int64_t width, void* out, const float* vpart,
+                         int64_t dense_rows, int64_t width, int64_t ld, void* out, const float* vpart,
                          float* slots, const int32_t* order, bool zero_counts, hipStream_t stream) {
 #define SPMM_BLOCK_CALL(T, I)                                                                   \
   return block_typed<T, I>(Crowptr, Ccol, Cvalue, windows, block_count, block_values, Vrowptr, \
-                           vector_rows, vector_nnz, dense, dense_rows, width, out, vpart, slots, \
+                           vector_rows, vector_nnz, dense, dense_rows, width, ld, out, vpart, slots, \
                            order, zero_counts, stream)
   if (value_type == SPMM_VALUE_F16) {
     if (index_type == SPMM_INDEX_I32) SPMM_BLOCK_CALL(_Float16, int32_t);

@@ -92,6 +92,24 @@ spmm_status check_csr_pointers(const spmm_csr_desc* d, const void* rowptr, const
   return check_aligned(dense, out, op);
 }
 
+int64_t elem_bytes(int32_t value_type) { return value_type == SPMM_VALUE_F16 ? 2 : 4; }
+
+// spmm_csr over column slabs of pass_width columns (one pass when the dense
+// operand is small): the same gather kernels per slab, rows N apart.
+spmm_status csr_passes(const spmm_csr_desc* d, const void* rowptr, const void* col, const void* value,
+                       const void* dense, void* out, void* ws, size_t ws_bytes, hipStream_t stream) {
+  const int64_t s = elem_bytes(d->value_type);
+  const int64_t w = pass_width(d->dense_rows, d->width, s);
+  for (int64_t c = 0; c < d->width; c += w) {
+    if (spmm_status st = launch_gather(d->index_type, d->value_type, rowptr, col, value, d->nnz, d->rows, 0,
+                                       d->rows, static_cast<const char*>(dense) + c * s, d->dense_rows, w,
+                                       d->width, static_cast<char*>(out) + c * s, ws, ws_bytes, nullptr, 0, 0,
+                                       nullptr, nullptr, nullptr, nullptr, 0, stream))
+      return st;
+  }
+  return SPMM_OK;
+}
+
 // Device address of `scratch` on the current device, resolved with
 // hipGetSymbolAddress on the first call per device (with that device
 // current) and kept; every later call on the device reuses it.
@@ -130,7 +148,8 @@ spmm_status spmm_csr_workspace(const spmm_csr_desc* d, size_t* bytes) {
   clear_error();
   if (d == nullptr || bytes == nullptr) return fail(SPMM_ERR_INVALID_ARGUMENT, "null argument");
   if (spmm_status st = check_types(d->index_type, d->value_type, "spmm_csr")) return st;
-  *bytes = gather_workspace_bytes(d->nnz < 0 ? 0 : d->nnz, d->width);
+  *bytes = gather_workspace_bytes(d->nnz < 0 ? 0 : d->nnz,
+                                  pass_width(d->dense_rows, d->width, elem_bytes(d->value_type)));
   return SPMM_OK;
 }
 
@@ -141,9 +160,7 @@ spmm_status spmm_csr_run(const spmm_csr_desc* d, const void* rowptr, const void*
   if (spmm_status st = check_csr_desc(d, "spmm_csr")) return st;
   if (d->rows == 0) return SPMM_OK;
   if (spmm_status st = check_csr_pointers(d, rowptr, col, value, dense, out, "spmm_csr")) return st;
-  return launch_gather(d->index_type, d->value_type, rowptr, col, value, d->nnz, d->rows, 0, d->rows,
-                       dense, d->dense_rows, d->width, out, workspace, workspace_bytes, nullptr, 0, 0,
-                       nullptr, nullptr, nullptr, nullptr, 0, as_stream(stream));
+  return csr_passes(d, rowptr, col, value, dense, out, workspace, workspace_bytes, as_stream(stream));
 }
 
 size_t spmm_csr_noalloc_max_scratch(void) { return kNoallocScratchBytes; }
@@ -154,7 +171,8 @@ spmm_status spmm_csr_run_noalloc(const spmm_csr_desc* d, const void* rowptr, con
   if (spmm_status st = check_csr_desc(d, "spmm_csr_run_noalloc")) return st;
   // The gather's scratch (tail rows, fp32 partial slots) must fit the fixed
   // array; checked before any HIP call.
-  const size_t need = gather_workspace_bytes(d->nnz, d->width);
+  const size_t need =
+      gather_workspace_bytes(d->nnz, pass_width(d->dense_rows, d->width, elem_bytes(d->value_type)));
   if (need > kNoallocScratchBytes)
     return fail(SPMM_ERR_CONTRACT, "spmm_csr_run_noalloc: this call needs " + std::to_string(need) +
                                        " bytes of scratch, more than the library's fixed " +
@@ -166,9 +184,7 @@ spmm_status spmm_csr_run_noalloc(const spmm_csr_desc* d, const void* rowptr, con
   if (spmm_status st = scratch_on_current_device(&ws)) return st;
   // Nothing in the scratch needs clearing: every call writes each tail entry
   // and each partial slot before the post pass reads it.
-  return launch_gather(d->index_type, d->value_type, rowptr, col, value, d->nnz, d->rows, 0, d->rows,
-                       dense, d->dense_rows, d->width, out, ws, kNoallocScratchBytes, nullptr, 0, 0,
-                       nullptr, nullptr, nullptr, nullptr, 0, as_stream(stream));
+  return csr_passes(d, rowptr, col, value, dense, out, ws, kNoallocScratchBytes, as_stream(stream));
 }
 
 spmm_status spmm_csr_rowscalar_run(const spmm_csr_desc* d, const void* rowptr, const void* col,
@@ -198,15 +214,17 @@ int64_t spmm_mixed_out_rows(const spmm_mixed_desc* d) {
 }
 
 namespace {
-// Workspace of the mixed operator: gather part, then the fp32 vector sums of
-// block-window rows ([16*windows][width]), then the pieces of windows longer
-// than the block chunk ([ranges][2][16][width]) and one counter per overflow
-// range ([ranges] uint32, zeroed by the call before the block kernel).
+// Workspace of the mixed operator, for one column pass of w = pass_width
+// columns (passes run one after another and reuse it): gather part, then the
+// fp32 vector sums of block-window rows ([16*windows][w]), then the pieces of
+// windows longer than the block chunk ([ranges][2][16][w]) and one counter per
+// overflow range ([ranges] uint32, zeroed by each pass before its block
+// kernel).
 struct MixedLayout {
   size_t gather = 0, vpart = 0, slots = 0, order = 0;
-  int64_t limit = 0, ranges = 0;
+  int64_t limit = 0, ranges = 0, w = 0;
   explicit MixedLayout(const spmm_mixed_desc* d) {
-    const int64_t w = d->width > 0 ? d->width : 0;
+    w = d->width > 0 ? pass_width(d->dense_rows, d->width, elem_bytes(d->value_type)) : 0;
     gather = align_up(gather_workspace_bytes(d->vector_nnz < 0 ? 0 : d->vector_nnz, w), 256);
     // vpart only when there is a vector part (rows of block windows may then
     // have vector sums to hand over).
@@ -276,15 +294,24 @@ spmm_status spmm_mixed_run(const spmm_mixed_desc* d, const void* Crowptr, const 
   // when the gather covers any row), else the block launch does.
   const int64_t row_lo = d->vector_nnz == 0 ? 16 * d->block_windows : 0;
   const bool gather_runs = out_rows > row_lo;
-  uint32_t* counts = reinterpret_cast<uint32_t*>(slots + lay.ranges * 2 * 16 * d->width);
-  spmm_status st = launch_gather(d->index_type, d->value_type, Vrowptr, Vcol, Vvalue, d->vector_nnz,
-                                 d->vector_rows, row_lo, out_rows, dense, d->dense_rows, d->width, out, ws,
-                                 lay.gather, d->block_windows > 0 ? Crowptr : nullptr, d->block_windows,
-                                 lay.limit, vpart, Ccol, order, lay.ranges > 0 ? counts : nullptr, lay.ranges, s);
-  if (st != SPMM_OK) return st;
-  return launch_block(d->index_type, d->value_type, Crowptr, Ccol, Cvalue, d->block_windows,
-                      d->block_count, d->block_values, Vrowptr, d->vector_rows, d->vector_nnz, dense,
-                      d->dense_rows, d->width, out, vpart, slots, order, !gather_runs, s);
+  // A dense operand much larger than the Infinity Cache is swept in column
+  // passes of lay.w columns (pass_width), each pass both parts on its slab.
+  uint32_t* counts = reinterpret_cast<uint32_t*>(slots + lay.ranges * 2 * 16 * lay.w);
+  const int64_t eb = elem_bytes(d->value_type);
+  for (int64_t c = 0; c < d->width; c += lay.w) {
+    const void* dense_c = static_cast<const char*>(dense) + c * eb;
+    void* out_c = static_cast<char*>(out) + c * eb;
+    spmm_status st = launch_gather(d->index_type, d->value_type, Vrowptr, Vcol, Vvalue, d->vector_nnz,
+                                   d->vector_rows, row_lo, out_rows, dense_c, d->dense_rows, lay.w, d->width, out_c,
+                                   ws, lay.gather, d->block_windows > 0 ? Crowptr : nullptr, d->block_windows,
+                                   lay.limit, vpart, Ccol, order, lay.ranges > 0 ? counts : nullptr, lay.ranges, s);
+    if (st != SPMM_OK) return st;
+    st = launch_block(d->index_type, d->value_type, Crowptr, Ccol, Cvalue, d->block_windows, d->block_count,
+                      d->block_values, Vrowptr, d->vector_rows, d->vector_nnz, dense_c, d->dense_rows, lay.w,
+                      d->width, out_c, vpart, slots, order, !gather_runs, s);
+    if (st != SPMM_OK) return st;
+  }
+  return SPMM_OK;
 }
 
 }  // extern "C"

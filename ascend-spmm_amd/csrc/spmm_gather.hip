@@ -204,17 +204,17 @@ struct BufferLoader {
   spmm_rsrc_t rsrc;
   uint32_t lane_bytes;  // c0 * sizeof(T)
   static constexpr uint32_t kNone = kBufferNone;
-  __device__ inline BufferLoader(const T* dense, int64_t K, int64_t N, int64_t c0) {
+  __device__ inline BufferLoader(const T* dense, int64_t K, int64_t ld, int64_t N, int64_t c0) {
     const uint64_t a = reinterpret_cast<uint64_t>(dense);
     rsrc[0] = static_cast<int>(a & 0xFFFFFFFFu);
     rsrc[1] = static_cast<int>((a >> 32) & 0xFFFFu);  // stride 0: raw buffer
-    rsrc[2] = static_cast<int>(static_cast<uint32_t>(K * N * static_cast<int64_t>(sizeof(T))));
+    rsrc[2] = static_cast<int>(static_cast<uint32_t>(buffer_extent(K, ld, N, sizeof(T))));
     rsrc[3] = 0x00020000;  // 32-bit data format; no swizzle, no thread-id offset
     lane_bytes = static_cast<uint32_t>(c0 * static_cast<int64_t>(sizeof(T)));
   }
-  __device__ static inline uint32_t stage(int64_t c, int64_t K, int64_t N) {
+  __device__ static inline uint32_t stage(int64_t c, int64_t K, int64_t ld) {
     return static_cast<uint64_t>(c) < static_cast<uint64_t>(K)
-               ? static_cast<uint32_t>(c) * static_cast<uint32_t>(N * static_cast<int64_t>(sizeof(T)))
+               ? static_cast<uint32_t>(c) * static_cast<uint32_t>(ld * static_cast<int64_t>(sizeof(T)))
                : kNone;
   }
   __device__ inline lanes::raw16_t load(uint32_t src) const {
@@ -227,16 +227,16 @@ struct BufferLoader {
 template <typename T>
 struct GlobalLoader {
   const T* dense_c0;  // dense + c0
-  uint32_t N;
+  uint32_t ld;        // row stride of dense (elements)
   static constexpr uint32_t kNone = kBadCol;
-  __device__ inline GlobalLoader(const T* dense, int64_t, int64_t n, int64_t c0)
-      : dense_c0(dense + c0), N(static_cast<uint32_t>(n)) {}
+  __device__ inline GlobalLoader(const T* dense, int64_t, int64_t ld_, int64_t, int64_t c0)
+      : dense_c0(dense + c0), ld(static_cast<uint32_t>(ld_)) {}
   __device__ static inline uint32_t stage(int64_t c, int64_t K, int64_t) {
     return static_cast<uint64_t>(c) < static_cast<uint64_t>(K) ? static_cast<uint32_t>(c) : kNone;
   }
   __device__ inline lanes::raw16_t load(uint32_t src) const {
     const bool ok = src != kNone;
-    const lanes::raw16_t x = lanes::load_raw16(dense_c0 + static_cast<uint64_t>(ok ? src : 0u) * N);
+    const lanes::raw16_t x = lanes::load_raw16(dense_c0 + static_cast<uint64_t>(ok ? src : 0u) * ld);
     const lanes::raw16_t zero = {0u, 0u, 0u, 0u};
     return ok ? x : zero;
   }
@@ -292,7 +292,7 @@ template <typename T>
 struct Sink {
   int64_t rS, row_hi;
   T* out;
-  int64_t N, c0;
+  int64_t N, ld, c0;  // vpart rows hold N floats; out rows are ld elements apart
   float* vpart;
   float* head_slot;
   float* tail_slot;
@@ -308,7 +308,7 @@ struct Sink {
 #pragma unroll
         for (int i = 0; i < V; ++i) dst[i] = acc[i];
       } else {
-        lanes::LaneVec<T>::store(out + row * N + c0, acc);
+        lanes::LaneVec<T>::store(out + row * ld + c0, acc);
       }
     }
     head = false;
@@ -461,7 +461,7 @@ __device__ void order_windows(const Geometry<I>& g, int32_t* cnt, int32_t* part)
 template <typename T, typename I, typename Loader, bool kOrder>
 __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM_GATHER_WAVES))) void gather_tiles(
     Geometry<I> g, const I* __restrict__ col, const T* __restrict__ value,
-    const T* __restrict__ dense, int64_t K, int64_t N, T* __restrict__ out, float* __restrict__ ws,
+    const T* __restrict__ dense, int64_t K, int64_t N, int64_t ld, T* __restrict__ out, float* __restrict__ ws,
     int log2L, int64_t chunks, int64_t ranges_per_tile, int64_t slot, int wg_split, int64_t tiles,
     int64_t tiles_per_group) {
   constexpr int V = LaneVec<T>::V;
@@ -536,7 +536,7 @@ __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM
     for (int k = 0; k < kStageUnroll; ++k) {
       const int64_t i = i0 + k * blockDim.x + threadIdx.x;
       if (i < tile_positions) {
-        const uint32_t src = Loader::stage(static_cast<int64_t>(cs[k]), K, N);
+        const uint32_t src = Loader::stage(static_cast<int64_t>(cs[k]), K, ld);
         sa.src[i] = src;
         sa.mark[i] = 0u;
         sa.val[i] = src != Loader::kNone ? value_bits<T>(vs[k]) : kNegZero<T>;
@@ -602,6 +602,7 @@ __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM
   sk.row_hi = g.row_hi;
   sk.out = out;
   sk.N = N;
+  sk.ld = ld;
   sk.c0 = c0;
   sk.vpart = g.vpart;
   sk.head_slot = ws + (2 * j) * slot + c0;
@@ -615,7 +616,7 @@ __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM
   // are issued before a batch is accumulated.  The first batch (4-aligned
   // start, positions before ps masked) and the last two are issued masked;
   // the steady-state loop only issues batches wholly inside [ps, pe).
-  const Stream<T, Loader> st{sa, Loader(dense, K, N, c0), ps, pe};
+  const Stream<T, Loader> st{sa, Loader(dense, K, ld, N, c0), ps, pe};
   int32_t p = ps & ~(kBatch - 1);
   Batch<T> A, B;
   st.template issue<true>(A, p);
@@ -651,7 +652,7 @@ __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM
 //  * the rest: empty rows, 64 per wavefront, are written as zeros (rows of
 //    block windows with blocks are left to the block kernel).
 template <typename T, typename I>
-__global__ __launch_bounds__(kWgThreads) void gather_post(Geometry<I> g, int64_t N, T* __restrict__ out,
+__global__ __launch_bounds__(kWgThreads) void gather_post(Geometry<I> g, int64_t N, int64_t ld, T* __restrict__ out,
                                                           const float* __restrict__ ws, int log2L,
                                                           int64_t chunks, int64_t slot, int64_t fix_blocks,
                                                           uint32_t* zero_counts, int64_t count, int64_t zero_blocks) {
@@ -709,7 +710,7 @@ __global__ __launch_bounds__(kWgThreads) void gather_post(Geometry<I> g, int64_t
 #pragma unroll
       for (int i = 0; i < V; ++i) dst[i] = acc[i];
     } else {
-      LaneVec<T>::store(out + r * N + c0, acc);
+      LaneVec<T>::store(out + r * ld + c0, acc);
     }
     return;
   }
@@ -729,7 +730,7 @@ __global__ __launch_bounds__(kWgThreads) void gather_post(Geometry<I> g, int64_t
       float z[V];
 #pragma unroll
       for (int i = 0; i < V; ++i) z[i] = 0.f;
-      LaneVec<T>::store(out + rr * N + c0, z);
+      LaneVec<T>::store(out + rr * ld + c0, z);
     }
   }
 }
@@ -737,7 +738,7 @@ __global__ __launch_bounds__(kWgThreads) void gather_post(Geometry<I> g, int64_t
 template <typename T, typename I>
 spmm_status gather_typed(const void* rowptr, const void* col, const void* value, int64_t nnz,
                          int64_t vrows, int64_t row_lo, int64_t row_hi, const void* dense, int64_t K,
-                         int64_t N, void* out, void* ws, size_t ws_bytes, const void* Crowptr,
+                         int64_t N, int64_t ld, void* out, void* ws, size_t ws_bytes, const void* Crowptr,
                          int64_t cwin, int64_t climit, float* vpart, const void* Ccol, int32_t* order,
                          uint32_t* zero_counts, int64_t count, hipStream_t stream) {
   constexpr int V = LaneVec<T>::V;
@@ -800,7 +801,7 @@ spmm_status gather_typed(const void* rowptr, const void* col, const void* value,
     size_t lds = static_cast<size_t>((ranges_per_tile + 1) * g.range) * Staged<T>::bytes_per_position();
     if (g.order && lds < (kOrderBuckets + 1024) * sizeof(int32_t)) lds = (kOrderBuckets + 1024) * sizeof(int32_t);
     // Dense operands within a 32-bit byte extent use buffer loads.
-    const bool buffer = K * N * static_cast<int64_t>(sizeof(T)) <= kBufferLimit;
+    const bool buffer = buffer_extent(K, ld, N, sizeof(T)) <= kBufferLimit;
     auto kernel = g.order ? (buffer ? gather_tiles<T, I, BufferLoader<T>, true> : gather_tiles<T, I, GlobalLoader<T>, true>)
                           : (buffer ? gather_tiles<T, I, BufferLoader<T>, false> : gather_tiles<T, I, GlobalLoader<T>, false>);
     // kXcds / wg_split groups of XCDs take runs of kXcdRun tiles in turn.
@@ -810,7 +811,7 @@ spmm_status gather_typed(const void* rowptr, const void* col, const void* value,
     hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(kXcds * tiles_per_group + (g.order ? kXcds : 0))),
                        dim3(static_cast<unsigned>(wg_threads)), lds, stream, g,
                        static_cast<const I*>(col), static_cast<const T*>(value),
-                       static_cast<const T*>(dense), K, N, static_cast<T*>(out), partial, log2L,
+                       static_cast<const T*>(dense), K, N, ld, static_cast<T*>(out), partial, log2L,
                        chunks, ranges_per_tile, slot, wg_split, tiles, tiles_per_group);
     if (spmm_status st = check_launch("gather_tiles")) return st;
   }
@@ -819,7 +820,7 @@ spmm_status gather_typed(const void* rowptr, const void* col, const void* value,
   const int64_t row_blocks = ceil_div(ceil_div(row_hi - row_lo, 64), kWgThreads / 64);
   const int64_t zero_blocks = zero_counts != nullptr ? ceil_div(count, kWgThreads) : 0;
   hipLaunchKernelGGL((gather_post<T, I>), dim3(static_cast<unsigned>(fix_blocks + zero_blocks + row_blocks)),
-                     dim3(kWgThreads), 0, stream, g, N, static_cast<T*>(out),
+                     dim3(kWgThreads), 0, stream, g, N, ld, static_cast<T*>(out),
                      static_cast<const float*>(partial), log2L, chunks, slot, fix_blocks, zero_counts, count,
                      zero_blocks);
   return check_launch("gather_post");
@@ -836,13 +837,13 @@ size_t gather_workspace_bytes(int64_t nnz, int64_t width) {
 spmm_status launch_gather(int32_t index_type, int32_t value_type, const void* rowptr,
                           const void* col, const void* value, int64_t nnz, int64_t vrows,
                           int64_t row_lo, int64_t row_hi, const void* dense, int64_t dense_rows,
-                          int64_t width, void* out, void* workspace, size_t workspace_bytes,
+                          int64_t width, int64_t ld, void* out, void* workspace, size_t workspace_bytes,
                           const void* Crowptr, int64_t cwin, int64_t climit, float* vpart,
                           const void* Ccol, int32_t* order, uint32_t* zero_counts, int64_t count,
                           hipStream_t stream) {
 #define SPMM_GATHER_CALL(T, I)                                                                 \
   return gather_typed<T, I>(rowptr, col, value, nnz, vrows, row_lo, row_hi, dense, dense_rows, \
-                            width, out, workspace, workspace_bytes, Crowptr, cwin, climit, vpart, \
+                            width, ld, out, workspace, workspace_bytes, Crowptr, cwin, climit, vpart, \
                             Ccol, order, zero_counts, count, stream)
   if (value_type == SPMM_VALUE_F16) {
     if (index_type == SPMM_INDEX_I32) SPMM_GATHER_CALL(_Float16, int32_t);

@@ -600,3 +600,44 @@ def test_windows_longer_than_the_block_chunk(spmm_npu, dtype, width):
         dev(h["vrow_window_ptr"], i32), dev(h["vcol_indices"], i32), dev(h["vvalue"]), dev(B),
         dev(O.make_start(h["crow_window_ptr"], 20)), dev(O.make_start(h["vrow_window_ptr"], 40)))
     assert_close(out[:rows], expected, dtype)
+
+
+@pytest.mark.parametrize("dtype", ["fp32", "fp16"])
+def test_column_passes_equal_single_pass_bitwise(spmm_npu, dtype):
+    """A dense operand of more than 512 MiB (K = 600k rows: fp32 N = 512, or
+    fp16 N = 1024) is swept in column passes (pass_width: 128 fp32 / 256 fp16
+    columns).  Each slab of the result equals a one-pass call on that slab
+    of the dense operand bit for bit, for spmm_csr and spmm_ascend_cube (a
+    block_level_split layout, block and vector parts), and matches fp64."""
+    K, rows = 600_000, 2048
+    N = 512 if dtype == "fp32" else 1024
+    w = 128 if dtype == "fp32" else 256
+    tdt = torch.float32 if dtype == "fp32" else torch.float16
+    rng = np.random.default_rng(97)
+    B = torch.empty((K, N), dtype=tdt, device="cuda")
+    B.normal_(generator=torch.Generator(device="cuda").manual_seed(9))
+    crow, col = random_csr(rng, rows, K, 60, long_rows=[(5, 3000), (1000, 700)])
+    vals = rng.uniform(-1, 1, col.size).astype(NP_DT[dtype])
+    i32 = torch.int32
+    start = dev(O.make_start(crow, 40))
+    full = spmm_npu.spmm_csr(dev(crow, i32), dev(col, i32), dev(vals), B, start)
+    h = O.block_level_split(crow, col, vals, rows, K, 0.5, 16)
+    mops = (dev(h["crow_window_ptr"], i32), dev(h["unique_col_ids"], i32), dev(h["value"]),
+            dev(h["vrow_window_ptr"], i32), dev(h["vcol_indices"], i32), dev(h["vvalue"]))
+    mstarts = (dev(O.make_start(h["crow_window_ptr"], 20)), dev(O.make_start(h["vrow_window_ptr"], 40)))
+    assert h["unique_col_ids"].size > 0 and h["vcol_indices"].size > 0
+    mfull = spmm_npu.spmm_ascend_cube(*mops, B, *mstarts)
+    for c in (0, N - w):
+        slab = B[:, c:c + w].contiguous()
+        one = spmm_npu.spmm_csr(dev(crow, i32), dev(col, i32), dev(vals), slab, start)
+        assert torch.equal(full[:, c:c + w], one), f"spmm_csr slab {c}"
+        mone = spmm_npu.spmm_ascend_cube(*mops, slab, *mstarts)
+        assert torch.equal(mfull[:, c:c + w], mone), f"spmm_ascend_cube slab {c}"
+        del slab
+    used = np.unique(col)
+    Bsub = B[:, :64][torch.from_numpy(used).cuda()].cpu().numpy()
+    expected = O.spmm_f64(crow, np.searchsorted(used, col), vals, Bsub)
+    assert_close(full[:, :64], expected, dtype)
+    assert_close(mfull[:rows, :64], expected, dtype)
+    del B
+    torch.cuda.empty_cache()
