@@ -114,6 +114,13 @@ inline bool block_order_wanted(int64_t windows, int64_t vector_nnz, int64_t widt
   return windows > 0 && windows <= kOrderMaxWindows && vector_nnz > 0 && row_bytes >= kOrderMinRowBytes;
 }
 
+// Gather-rate probe (measurement): the gather path's dense-row loads over
+// the same nonzeros, without rows or output; int32 column ids.
+size_t gather_probe_sink_floats(int64_t nnz, int64_t width, int32_t value_type);
+spmm_status launch_gather_probe(int32_t value_type, const void* col, const void* value, int64_t nnz,
+                                const void* dense, int64_t dense_rows, int64_t width, float* sink,
+                                hipStream_t stream);
+
 // Thread-per-row scalar CSR baseline over rows [0, rows) (no workspace).
 spmm_status launch_rowscalar(int32_t index_type, int32_t value_type, const void* rowptr, const void* col,
                              const void* value, int64_t rows, int64_t nnz, const void* dense, int64_t K,

@@ -187,6 +187,24 @@ spmm_status spmm_csr_run_noalloc(const spmm_csr_desc* d, const void* rowptr, con
   return csr_passes(d, rowptr, col, value, dense, out, ws, kNoallocScratchBytes, as_stream(stream));
 }
 
+size_t spmm_gather_probe_sink(const spmm_csr_desc* d) {
+  if (d == nullptr || d->nnz < 0 || d->width <= 0) return 0;
+  return gather_probe_sink_floats(d->nnz, d->width, d->value_type);
+}
+
+spmm_status spmm_gather_probe(const spmm_csr_desc* d, const void* col, const void* value, const void* dense,
+                              float* sink, spmm_stream stream) {
+  clear_error();
+  if (spmm_status st = check_csr_desc(d, "spmm_gather_probe")) return st;
+  if (d->index_type != SPMM_INDEX_I32) return fail(SPMM_ERR_CONTRACT, "spmm_gather_probe: int32 column ids only");
+  if (d->nnz == 0) return SPMM_OK;
+  if (col == nullptr || value == nullptr || dense == nullptr || sink == nullptr)
+    return fail(SPMM_ERR_INVALID_ARGUMENT, "spmm_gather_probe: null device pointer");
+  if (spmm_status st = check_aligned(dense, sink, "spmm_gather_probe")) return st;
+  return launch_gather_probe(d->value_type, col, value, d->nnz, dense, d->dense_rows, d->width, sink,
+                             as_stream(stream));
+}
+
 spmm_status spmm_csr_rowscalar_run(const spmm_csr_desc* d, const void* rowptr, const void* col,
                                    const void* value, const void* dense, void* out, spmm_stream stream) {
   clear_error();

@@ -735,6 +735,124 @@ __global__ __launch_bounds__(kWgThreads) void gather_post(Geometry<I> g, int64_t
   }
 }
 
+// Gather-rate probe (measurement only, never part of an SpMM): the dense-row
+// gathers of gather_tiles over the same nonzeros and ranges -- staged column
+// ids and values, one raw buffer load of 16 bytes per lane per nonzero, two
+// batches of 4 in flight, fp32 FMAs -- without the row search, marks,
+// partial sums or output rows.  Each thread writes its sum to sink (so the
+// loads stay live).  Its time bounds what the gather path can reach on the
+// input: the ceiling bench.py reports beside the SpMM's rate.
+template <typename T>
+__global__ __launch_bounds__(kWgThreads) void gather_probe(const int32_t* __restrict__ col,
+                                                           const T* __restrict__ value, int64_t nnz,
+                                                           const T* __restrict__ dense, int64_t K, int64_t N,
+                                                           int log2L, int64_t range, float* __restrict__ sink) {
+  constexpr int V = LaneVec<T>::V;
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int64_t groups = static_cast<int64_t>(blockDim.x) >> log2L;
+  const int64_t tile_positions = groups * range;
+  const Staged<T> sa(smem, tile_positions);
+  const int64_t P0 = static_cast<int64_t>(blockIdx.x) * tile_positions;
+  for (int64_t i0 = 0; i0 < tile_positions; i0 += kStageUnroll * blockDim.x) {
+    int32_t cs[kStageUnroll];
+    T vs[kStageUnroll];
+#pragma unroll
+    for (int k = 0; k < kStageUnroll; ++k) {
+      const int64_t p = P0 + i0 + k * blockDim.x + threadIdx.x;
+      cs[k] = p < nnz ? col[p] : -1;
+      vs[k] = p < nnz ? value[p] : static_cast<T>(0);
+    }
+#pragma unroll
+    for (int k = 0; k < kStageUnroll; ++k) {
+      const int64_t i = i0 + k * blockDim.x + threadIdx.x;
+      if (i < tile_positions) {
+        const uint32_t src = BufferLoader<T>::stage(static_cast<int64_t>(cs[k]), K, N);
+        sa.src[i] = src;
+        sa.mark[i] = 0u;
+        sa.val[i] = src != BufferLoader<T>::kNone ? value_bits<T>(vs[k]) : kNegZero<T>;
+      }
+    }
+  }
+  __syncthreads();
+  const int group = threadIdx.x >> log2L;
+  const int lane = threadIdx.x & ((1 << log2L) - 1);
+  const int32_t ps = static_cast<int32_t>(group * range);
+  const int64_t left = nnz - P0 - ps;
+  const int32_t pe = ps + static_cast<int32_t>(left < range ? left : range);
+  float acc[V];
+#pragma unroll
+  for (int i = 0; i < V; ++i) acc[i] = 0.f;
+  if (left > 0 && static_cast<int64_t>(lane) * V < N) {
+    const Stream<T, BufferLoader<T>> st{sa, BufferLoader<T>(dense, K, N, N, static_cast<int64_t>(lane) * V), ps, pe};
+    auto consume = [&](const Batch<T>& b) {
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        float x[V];
+        LaneVec<T>::unpack(b.x[u], x);
+#pragma unroll
+        for (int i = 0; i < V; ++i) acc[i] = __builtin_fmaf(b.v[u], x[i], acc[i]);
+      }
+    };
+    int32_t p = ps;
+    Batch<T> A, B;
+    st.template issue<true>(A, p);
+    for (; p + 3 * kBatch <= pe; p += 2 * kBatch) {
+      st.template issue<false>(B, p + kBatch);
+      consume(A);
+      st.template issue<false>(A, p + 2 * kBatch);
+      consume(B);
+    }
+    if (p + kBatch < pe) {
+      st.template issue<true>(B, p + kBatch);
+      consume(A);
+      if (p + 2 * kBatch < pe) {
+        st.template issue<true>(A, p + 2 * kBatch);
+        consume(B);
+        consume(A);
+      } else {
+        consume(B);
+      }
+    } else {
+      consume(A);
+    }
+  }
+  float sum = 0.f;
+#pragma unroll
+  for (int i = 0; i < V; ++i) sum += acc[i];
+  sink[static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x] = sum;
+}
+
+// Geometry of the probe launch: lane-group width, ranges per work-group
+// (the gather path's R), work-groups and sink floats.
+struct ProbeGeometry {
+  int log2L = 0;
+  int64_t range = 0, groups = 0, blocks = 0;
+  ProbeGeometry(int64_t nnz, int64_t N, int64_t elem_bytes) {
+    const int64_t lanes_needed = N / (16 / elem_bytes);
+    while ((int64_t(1) << log2L) < lanes_needed && log2L < 6) ++log2L;
+    range = gather_range(nnz);
+    groups = kWgThreads >> log2L;
+    blocks = nnz > 0 ? ceil_div(ceil_div(nnz, range), groups) : 0;
+  }
+  int64_t sink_floats() const { return blocks * kWgThreads; }
+};
+
+template <typename T>
+spmm_status probe_typed(const void* col, const void* value, int64_t nnz, const void* dense, int64_t K, int64_t N,
+                        float* sink, hipStream_t stream) {
+  const ProbeGeometry pg(nnz, N, sizeof(T));
+  if (pg.blocks == 0) return SPMM_OK;
+  if (N > (int64_t(16) << 6) / static_cast<int64_t>(sizeof(T)))
+    return fail(SPMM_ERR_CONTRACT, "spmm_gather_probe: rows wider than 64 lanes");
+  if (buffer_extent(K, N, N, sizeof(T)) > kBufferLimit)
+    return fail(SPMM_ERR_CONTRACT, "spmm_gather_probe: dense operand beyond 4 GB");
+  const size_t lds = static_cast<size_t>(pg.groups * pg.range) * Staged<T>::bytes_per_position();
+  hipLaunchKernelGGL((gather_probe<T>), dim3(static_cast<unsigned>(pg.blocks)), dim3(kWgThreads), lds, stream,
+                     static_cast<const int32_t*>(col), static_cast<const T*>(value), nnz,
+                     static_cast<const T*>(dense), K, N, pg.log2L, pg.range, sink);
+  return check_launch("gather_probe");
+}
+
 template <typename T, typename I>
 spmm_status gather_typed(const void* rowptr, const void* col, const void* value, int64_t nnz,
                          int64_t vrows, int64_t row_lo, int64_t row_hi, const void* dense, int64_t K,
@@ -832,6 +950,18 @@ size_t gather_workspace_bytes(int64_t nnz, int64_t width) {
   const int64_t nr = (nnz > 0 ? ceil_div(nnz, gather_range(nnz)) : 1);
   return align_up(static_cast<size_t>(nr) * sizeof(int64_t), 256) +
          static_cast<size_t>(2 * nr) * gather_slot_floats(width) * sizeof(float);
+}
+
+size_t gather_probe_sink_floats(int64_t nnz, int64_t width, int32_t value_type) {
+  return static_cast<size_t>(ProbeGeometry(nnz, width, value_type == SPMM_VALUE_F16 ? 2 : 4).sink_floats());
+}
+
+spmm_status launch_gather_probe(int32_t value_type, const void* col, const void* value, int64_t nnz,
+                                const void* dense, int64_t dense_rows, int64_t width, float* sink,
+                                hipStream_t stream) {
+  if (value_type == SPMM_VALUE_F16)
+    return probe_typed<_Float16>(col, value, nnz, dense, dense_rows, width, sink, stream);
+  return probe_typed<float>(col, value, nnz, dense, dense_rows, width, sink, stream);
 }
 
 spmm_status launch_gather(int32_t index_type, int32_t value_type, const void* rowptr,

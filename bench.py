@@ -30,6 +30,8 @@ from __future__ import annotations
 
 import argparse
 import ctypes
+import glob
+import hashlib
 import json
 import os
 import sys
@@ -54,8 +56,9 @@ MFMA_PEAK_TFLOPS = {"fp16": 2500.0, "fp32": 157.3}
 # for a plain 256 MiB device copy (--copy-calibration: FETCH_SIZE reads 0.5 x
 # the bytes copied, WRITE_SIZE 1.0 x).  The counters see L2-to-fabric
 # traffic, Infinity Cache hits included.  Keyed by (config, op, width); the
-# runs are summarised in profiles/*_traffic.md.  Re-measured whenever the
-# kernels change.
+# runs are summarised in profiles/*_traffic.md.  Each entry records the hash
+# of the kernel sources it was measured on (kernel_sources_hash); when the
+# sources differ, the line reports traffic null with the reason.
 # The kernels one timed call launches (the roofline's event time covers all
 # of them, in launch order on one stream).
 OP_KERNELS = {
@@ -68,14 +71,31 @@ OP_KERNELS = {
 }
 FETCH_SCALE = 2.0
 WRITE_SCALE = 1.0
-PMC_KIB = {
-    (2, "csr", 128): {"fetch_kib": 203962.3 + 3879.9, "write_kib": 31384.1 + 659.8},
-    (3, "mixed", 128): {"fetch_kib": 51560.2 + 6313.1 + 130417.2 + 52.6,
-                        "write_kib": 12091.3 + 2266.5 + 14135.7 + 0.0},
-    (3, "bcsr", 128): {"fetch_kib": 47337.4 + 58.0, "write_kib": 16403.8 + 0.0},
-    (4, "mixed", 512): {"fetch_kib": 215823.9 + 5290.2 + 188080.1 + 30.0,
-                        "write_kib": 114565.9 + 2119.0 + 92312.1 + 0.0},
-}
+PMC_KIB = {}
+
+
+def kernel_sources_hash() -> str:
+    """sha256 (first 16 hex digits) of the library's kernel sources: the
+    HIP files and headers under ascend-spmm_amd/csrc, by name and content."""
+    h = hashlib.sha256()
+    csrc = os.path.join(REPO, "ascend-spmm_amd", "csrc")
+    for path in sorted(glob.glob(os.path.join(csrc, "*.hip")) + glob.glob(os.path.join(csrc, "*.h"))):
+        h.update(os.path.basename(path).encode())
+        with open(path, "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
+
+
+def measured_traffic(config: int, op: str, width: int):
+    """(bytes per call, note): the PMC table's traffic when it was measured on
+    the current kernel sources, else (None, the reason)."""
+    pmc = PMC_KIB.get((config, op, width))
+    if pmc is None:
+        return None, "no counter run for this configuration"
+    if pmc["sources"] != kernel_sources_hash():
+        return None, f"stale: kernel sources changed since the counter run ({pmc['profile']})"
+    return int(1024 * (pmc["fetch_kib"] * FETCH_SCALE + pmc["write_kib"] * WRITE_SCALE)), pmc["profile"]
+
 
 def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
@@ -215,11 +235,36 @@ class _CsrDesc(ctypes.Structure):
                 ("width", ctypes.c_int64), ("index_type", ctypes.c_int32), ("value_type", ctypes.c_int32)]
 
 
+LIBRARY = os.path.join(REPO, "ascend-spmm_amd", "libspmm_mi355x.so")
+
+
+def gather_ceiling_ms(col, val, dense, w, steps: int, warmup: int) -> float:
+    """HIP-event ms per call of the gather-rate probe (spmm_gather_probe of the
+    C ABI): the gather path's dense-row loads over the same nonzeros and
+    ranges, without rows, partial sums or output rows.  Its rate is the
+    ceiling of the gather path on this input and GPU."""
+    lib = ctypes.CDLL(LIBRARY)
+    lib.spmm_last_error.restype = ctypes.c_char_p
+    lib.spmm_gather_probe_sink.restype = ctypes.c_size_t
+    d = _CsrDesc(w.rows, w.nnz, w.cols, dense.shape[1], 0, 0 if dense.dtype == torch.float16 else 1)
+    sink = torch.empty(max(int(lib.spmm_gather_probe_sink(ctypes.byref(d))), 4), dtype=torch.float32,
+                       device=dense.device)
+    p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def step():
+        rc = lib.spmm_gather_probe(ctypes.byref(d), p(col), p(val), p(dense), p(sink), stream)
+        if rc != 0:
+            raise RuntimeError(lib.spmm_last_error().decode())
+
+    return time_calls(step, steps, warmup)[1]
+
+
 def rowscalar_ms(crow, col, val, dense, w) -> float:
     """HIP-event ms per call of the thread-per-row scalar CSR baseline
     (spmm_csr_rowscalar_run of the C ABI; one thread per output row), 1
     warm-up and 3 timed calls."""
-    lib = ctypes.CDLL(os.path.join(REPO, "ascend-spmm_amd", "libspmm_mi355x.so"))
+    lib = ctypes.CDLL(LIBRARY)
     lib.spmm_last_error.restype = ctypes.c_char_p
     out = torch.empty(w.rows, dense.shape[1], dtype=dense.dtype, device=dense.device)
     d = _CsrDesc(w.rows, w.nnz, w.cols, dense.shape[1], 0, 0 if dense.dtype == torch.float16 else 1)
@@ -475,14 +520,15 @@ def main() -> int:
 
     copy_rate = copy_gbps(1 << 30, 5, 1)[1]
     log(f"[bench] 1 GiB device copy: {copy_rate:.1f} GB/s (read + write)")
+    ceiling_ms = None
+    if args.op == "csr":
+        ceiling_ms = gather_ceiling_ms(col, val, dense, w, args.steps, args.warmup)
+        log(f"[bench] gather-rate probe {ceiling_ms:.4f} ms/call")
 
     flops = 2.0 * w.nnz * width
     t_s = wall_ms / 1e3
     achieved = alg_bytes / (event_ms / 1e3) / 1e9
-    pmc = PMC_KIB.get((args.config, args.op, width))
-    traffic = None
-    if pmc is not None:
-        traffic = int(1024 * (pmc["fetch_kib"] * FETCH_SCALE + pmc["write_kib"] * WRITE_SCALE))
+    traffic, traffic_source = measured_traffic(args.config, args.op, width)
     s_b = 2 if w.dtype == "fp16" else 4
     result = {
         "metric": METRIC,
@@ -514,6 +560,8 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": traffic,
+            "traffic_source": traffic_source,
+            "kernel_sources_hash": kernel_sources_hash(),
             "traffic_gbps": None if traffic is None else round(traffic / (event_ms / 1e3) / 1e9, 1),
             "traffic_frac": None if traffic is None else round(traffic / (event_ms / 1e3) / 1e9 / HBM_PEAK_GBPS, 4),
             "copy_gbps": round(copy_rate, 1),
@@ -521,6 +569,14 @@ def main() -> int:
             "algorithmic_bytes_per_call": alg_bytes,
             "gather_model_bytes": int(w.nnz * width * s_b),
             "event_ms_per_call": round(event_ms, 5),
+            # The gather-rate probe (op csr): the same dense-row loads without
+            # rows or output; its algorithmic-byte rate is the gather path's
+            # ceiling on this input and GPU.
+            "ceiling_ms_per_call": None if ceiling_ms is None else round(ceiling_ms, 5),
+            "ceiling_gbps": None if ceiling_ms is None else round(alg_bytes / (ceiling_ms / 1e3) / 1e9, 1),
+            "frac_of_ceiling": None if ceiling_ms is None else round(ceiling_ms / event_ms, 4),
+            "ceiling_gather_model_gbps": None if ceiling_ms is None else round(
+                w.nnz * width * s_b / (ceiling_ms / 1e3) / 1e9, 1),
         },
     }
     if not args.no_block_path and args.config == 2 and args.op == "csr":

@@ -110,6 +110,19 @@ spmm_status spmm_csr_run_noalloc(const spmm_csr_desc* desc,
                                  const void* rowptr, const void* col, const void* value,
                                  const void* dense, void* out, spmm_stream stream);
 
+/* Gather-rate probe.  No counterpart in the reference: a measurement for
+ * callers judging spmm_csr_run against what the GPU can gather.  It runs the
+ * dense-row gathers of spmm_csr_run over the same nonzeros (column ids and
+ * values staged per tile, one 16-byte piece of every nonzero's dense row per
+ * lane, fp32 FMAs) without the row bookkeeping, partial sums or output rows,
+ * and writes one float per thread to `sink` (spmm_gather_probe_sink(desc)
+ * floats, 16-byte aligned).  int32 column ids; dense operand up to 4 GB;
+ * rowptr is not read. */
+size_t spmm_gather_probe_sink(const spmm_csr_desc* desc);
+
+spmm_status spmm_gather_probe(const spmm_csr_desc* desc, const void* col, const void* value,
+                              const void* dense, float* sink, spmm_stream stream);
+
 /* Thread-per-row scalar CSR SpMM, same arguments and result contract as
  * spmm_csr_run (same sums in the same order within a row; no workspace).
  * No counterpart in the reference: it is the baseline that the block path's

@@ -82,3 +82,26 @@ def test_bench_preprocess_line():
         assert p["ms"] > 0 and p["bytes"] > 0 and p["cpu_ms"] > 0
     assert d["cpu_baseline"]["kind"] == "port" and d["cpu_baseline"]["cores"] == 1
     assert d["roofline"]["bound"] == "hbm" and d["value"] > 0
+
+
+def test_traffic_table_is_keyed_to_the_kernel_sources():
+    """roofline.traffic comes from the PMC table only when the entry was
+    measured on the current kernel sources (their hash); otherwise it is
+    null with the reason, never a stale figure."""
+    import sys
+
+    sys.path.insert(0, REPO)
+    import bench
+
+    h = bench.kernel_sources_hash()
+    assert len(h) == 16 and h == bench.kernel_sources_hash()
+    key = (99, "csr", 16)
+    bench.PMC_KIB[key] = {"fetch_kib": 1.0, "write_kib": 3.0, "sources": h, "profile": "profiles/x.md"}
+    try:
+        assert bench.measured_traffic(*key) == (1024 * (2 * 1 + 3), "profiles/x.md")
+        bench.PMC_KIB[key]["sources"] = "0" * 16
+        traffic, note = bench.measured_traffic(*key)
+        assert traffic is None and note.startswith("stale")
+    finally:
+        del bench.PMC_KIB[key]
+    assert bench.measured_traffic(98, "csr", 16)[0] is None
