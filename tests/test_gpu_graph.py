@@ -69,3 +69,113 @@ def test_spmm_ascend_cube_graph_replays(spmm_npu, graph_layout):
             dev(vcol, i32), dev(p["vvalue"]), B, dev(O.make_start(p["crow_window_ptr"], 20)),
             dev(O.make_start(p["vrow_window_ptr"], 40)))
     check_replays(spmm_npu.spmm_ascend_cube, args, B)
+
+
+# ---- C ABI calls under capture (ctypes, the current stream's handle) -------
+
+import ctypes  # noqa: E402
+import os  # noqa: E402
+
+from test_cabi import CsrDesc  # noqa: E402
+
+LIB = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "ascend-spmm_amd",
+                   "libspmm_mi355x.so")
+
+
+class CubeOpDesc(ctypes.Structure):
+    _fields_ = [("windows", ctypes.c_int64), ("nnz", ctypes.c_int64), ("dense_rows", ctypes.c_int64),
+                ("width", ctypes.c_int64), ("index_type", ctypes.c_int32), ("value_type", ctypes.c_int32)]
+
+
+@pytest.fixture(scope="module")
+def lib():
+    h = ctypes.CDLL(LIB)
+    h.spmm_last_error.restype = ctypes.c_char_p
+    h.spmm_pack_workspace.restype = ctypes.c_size_t
+    return h
+
+
+def _p(t):
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _ok(lib, rc):
+    assert rc == 0, lib.spmm_last_error()
+
+
+def test_cabi_spmm_cube_op_graph_replays(spmm_npu, lib):
+    """spmm_cube_op_run (window-encoded decode + MFMA block kernel) captured."""
+    rng = np.random.default_rng(5)
+    n, K = 400, 300
+    deg = rng.integers(0, 25, n)
+    crow = np.concatenate([[0], np.cumsum(deg)]).astype(np.int64)
+    col = np.concatenate([np.sort(rng.choice(K, d, replace=False)) for d in deg]).astype(np.int64)
+    val = rng.uniform(-1, 1, col.size).astype(np.float16)
+    rp, enc, v = O.cube_encode(crow, col, val, n)
+    d_rp, d_enc, d_v = dev(rp, torch.int32), dev(enc, torch.int32), dev(v)
+    B = torch.zeros(K, 64, dtype=torch.float16, device="cuda")
+    d = CubeOpDesc(rp.size - 1, enc.size, K, 64, 0, 0)
+    need = ctypes.c_size_t(0)
+    _ok(lib, lib.spmm_cube_op_workspace(ctypes.byref(d), ctypes.byref(need)))
+
+    def op(dense):
+        out = torch.empty(16 * (rp.size - 1), 64, dtype=torch.float16, device="cuda")
+        ws = torch.empty(max(need.value, 1), dtype=torch.uint8, device="cuda")
+        _ok(lib, lib.spmm_cube_op_run(ctypes.byref(d), _p(d_rp), _p(d_enc), _p(d_v), _p(dense), _p(out), _p(ws),
+                                      ctypes.c_size_t(need.value), _stream()))
+        return out
+
+    out = check_replays(op, (B,), B)
+    assert torch.equal(out, spmm_npu.spmm_cube(d_rp, d_enc, d_v, B, torch.zeros(20, dtype=torch.int32,
+                                                                                    device="cuda")))
+
+
+def test_cabi_pack_restore_graph_replays(spmm_npu, lib):
+    """spmm_pack_rows and spmm_restore_rows captured (the Python
+    pack_node_tensor / restore_node_tensor check inv_permutation on the host,
+    which reads the device, so the C ABI calls are the capturable form)."""
+    rng = np.random.default_rng(6)
+    rows, packed_rows, width = 300, 320, 48
+    inv = dev(rng.permutation(packed_rows)[:rows].astype(np.int64))
+    X = torch.zeros(rows, width, dtype=torch.float32, device="cuda")
+    row_bytes = width * 4
+    need = lib.spmm_pack_workspace(ctypes.c_int64(packed_rows))
+
+    def pack(src):
+        packed = torch.empty(packed_rows, width, device="cuda")
+        ws = torch.empty(max(need, 1), dtype=torch.uint8, device="cuda")
+        _ok(lib, lib.spmm_pack_rows(_p(src), ctypes.c_int64(rows), ctypes.c_int64(row_bytes), _p(inv), _p(packed),
+                                    ctypes.c_int64(packed_rows), _p(ws), ctypes.c_size_t(need), _stream()))
+        return packed
+
+    def restore(src):
+        out = torch.empty(rows, width, device="cuda")
+        _ok(lib, lib.spmm_restore_rows(_p(pack(src)), ctypes.c_int64(packed_rows), ctypes.c_int64(row_bytes),
+                                       _p(inv), ctypes.c_int64(rows), _p(out), _stream()))
+        return out
+
+    packed = check_replays(pack, (X,), X)
+    assert torch.equal(packed, spmm_npu.pack_node_tensor(X, inv.cpu(), packed_rows))
+    back = check_replays(restore, (X,), X)
+    assert torch.equal(back, X)
+
+
+def test_cabi_noalloc_graph_replays(spmm_npu, lib):
+    """spmm_csr_run_noalloc (library scratch, nothing allocated) captured."""
+    w = W.config2(scale=0.05)
+    B = dev(w.dense(128))
+    d = CsrDesc(w.rows, w.nnz, w.cols, 128, 0, 0)
+    crow, col, val = dev(w.crow, torch.int32), dev(w.col, torch.int32), dev(w.values)
+
+    def op(dense):
+        out = torch.empty(w.rows, 128, dtype=torch.float16, device="cuda")
+        _ok(lib, lib.spmm_csr_run_noalloc(ctypes.byref(d), _p(crow), _p(col), _p(val), _p(dense), _p(out),
+                                          _stream()))
+        return out
+
+    out = check_replays(op, (B,), B)
+    assert torch.equal(out, spmm_npu.spmm_csr(crow, col, val, B, dev(O.make_start(w.crow, 40))))
