@@ -3,9 +3,11 @@
 //   extension/boundary_bucket_sort.h   (stable_bucket_sort_by_occupancy_desc)
 //   extension/packed_column_reindex.h  (renumber_columns_for_packed_layout,
 //                                       transpose_into_packed_layout)
-// TEST INFRASTRUCTURE ONLY: built into oracle/_ref/ (never committed, never
-// shipped) and used by tests to pin the oracle's restatement of these three
-// functions against the reference's code.  Exceptions become status codes:
+// TEST INFRASTRUCTURE ONLY: built into oracle/_ref/ (never committed; the
+// built library travels with the working tree to the GPU box like the other
+// built libraries, but only the CPU tests load it) and used by tests to pin
+// the oracle's restatement of these three functions against the reference's
+// code.  Exceptions become status codes:
 // 1 invalid_argument, 2 out_of_range, 3 overflow_error.
 #include <cstdint>
 #include <cstring>
