@@ -100,15 +100,28 @@ spmm_status launch_gather(int32_t index_type, int32_t value_type,
                           const void* Ccol, int32_t* order, uint32_t* zero_counts, int64_t count,
                           hipStream_t stream);
 
-// Locality order of the block windows: with `order` set, one extra
-// work-group of the gather kernel, running beside the gathers, sorts the cwin
-// windows into kOrderBuckets buckets of their first block column (Ccol), and
-// the block kernel follows that order.  Used for at most kOrderMaxWindows
-// windows, dense rows of at least kOrderMinRowBytes, and a vector part (the
-// gather kernel runs).
+// Locality order of the block windows: with `order` set (2 * cwin int32:
+// the order, then one sort key per window), extra work-groups of the gather
+// kernel, running beside the gathers, write each window's key (its first
+// block column's bucket of kOrderBuckets, and whether the window is local),
+// the post pass's first work-group sorts the windows by key, and the block
+// kernel follows that order.  Used for at most kOrderMaxWindows windows,
+// dense rows of at least kOrderMinRowBytes (fp16 N >= 128, fp32 N >= 64),
+// and a vector part (the gather kernel runs).
 constexpr int64_t kOrderMaxWindows = 16384;
 constexpr int kOrderBuckets = 1024;
-constexpr int64_t kOrderMinRowBytes = 512;
+#ifndef SPMM_ORDER_MIN_ROW_BYTES
+#define SPMM_ORDER_MIN_ROW_BYTES 256
+#endif
+constexpr int64_t kOrderMinRowBytes = SPMM_ORDER_MIN_ROW_BYTES;
+
+// Window positions -> XCDs in the block kernel: XCDs take runs of this many
+// consecutive positions in turn (work-group g runs on XCD g % kXcds).
+#ifndef SPMM_BLOCK_XCD_RUN
+#define SPMM_BLOCK_XCD_RUN 32
+#endif
+constexpr int64_t kBlockXcdRun = SPMM_BLOCK_XCD_RUN;
+
 inline bool block_order_wanted(int64_t windows, int64_t vector_nnz, int64_t width, int32_t value_type) {
   const int64_t row_bytes = width * (value_type == SPMM_VALUE_F16 ? 2 : 4);
   return windows > 0 && windows <= kOrderMaxWindows && vector_nnz > 0 && row_bytes >= kOrderMinRowBytes;

@@ -72,13 +72,6 @@ typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 
-// XCD-aware window order: XCDs take runs of this many consecutive windows in
-// turn, so neighbouring windows share an L2 while windows of every density
-// (the preprocess layout sorts them by density) spread over all XCDs.
-#ifndef SPMM_BLOCK_XCD_RUN
-#define SPMM_BLOCK_XCD_RUN 16
-#endif
-constexpr int64_t kBlockXcdRun = SPMM_BLOCK_XCD_RUN;
 // Waves per window work-group: one per column group, up to this many (the
 // rest loop), so wide outputs do not lengthen each wave's chain of K-steps.
 #ifndef SPMM_BLOCK_MAX_WAVES

@@ -106,11 +106,13 @@ struct Geometry {
   const I* Crowptr;
   int64_t cwin, climit;
   float* vpart;
-  // Locality order of the block windows, written by the gather kernel's extra
-  // work-group when set.
+  // Locality order of the block windows when set: gather_tiles' extra
+  // work-groups write one key per window (keys, cwin entries), gather_post's
+  // first work-group sorts the windows by key into order (cwin entries).
   const I* Ccol;
   int64_t K;
   int32_t* order;
+  int32_t* keys;
 
   __device__ inline int64_t rp(int64_t r) const {
     return clampi(static_cast<int64_t>(rowptr[r < vrows ? r : vrows]), 0, nnz);
@@ -363,94 +365,134 @@ __device__ inline int64_t find_row(const Geometry<I>& g, int64_t P) {
   return lo;
 }
 
-// Locality order of the cwin block windows (one work-group of any size from
-// 32 threads, LDS: kOrderBuckets + 1024 int32): a counting sort by the
-// window's first block column in kOrderBuckets buckets over [0, K).  Windows
-// that gather the same dense rows end up next to each other, and the block
-// kernel deals consecutive positions of the order to one XCD.  Any
-// permutation gives the same results (every window is summed by its own
-// work-group), so ties within a bucket take the order of the LDS atomics.
+// Locality order of the cwin block windows: a counting sort by the window's
+// first block column in kOrderBuckets buckets over [0, K).  Windows that
+// gather the same dense rows end up next to each other, and the block kernel
+// deals runs of consecutive positions of the order to the XCDs in turn, so
+// the XCDs sweep the dense operand together and each XCD's L2 holds the rows
+// its next windows need.  Any permutation
+// gives the same results (every window is summed by its own work-group), so
+// ties within a bucket take the order of the LDS atomics.
 //
 // The order only pays where windows are local (their block columns span a
 // small part of [0, K), as in banded or clustered matrices).  When fewer than
 // half the windows span less than K / kOrderLocalDiv columns, the identity
 // order is written instead.
+//
+// Two steps, so that neither sits on the critical path of its kernel:
+//  * window_keys, in gather_tiles' kXcds extra work-groups beside the
+//    gathers: each work-group reads the block range and the first and last
+//    block column of its share of the windows (two dependent rounds of
+//    loads) and writes key = bucket | kKeyLocal when the window is local;
+//  * sort_windows, in gather_post's first work-group: a histogram of the
+//    keys in LDS, a scan, and the scatter into the order (the keys, 4 bytes
+//    per window, are read twice, from L2).
 constexpr int64_t kOrderLocalDiv = 8;
+constexpr int32_t kKeyLocal = 1 << 20;
+static_assert(kOrderBuckets < kKeyLocal, "bucket ids fit below the local bit");
 
 template <typename I>
-__device__ void order_windows(const Geometry<I>& g, int32_t* cnt, int32_t* part) {
+__device__ void window_keys(const Geometry<I>& g, int64_t part) {
+  const int64_t share = (g.cwin + kXcds - 1) / kXcds;
+  const int64_t s_lo = part * share;
+  const int64_t s_hi = s_lo + share < g.cwin ? s_lo + share : g.cwin;
+  const int64_t nt = blockDim.x;
+  constexpr int kU = 4;  // windows per thread per round, their loads issued together
+  for (int64_t s0 = s_lo; s0 < s_hi; s0 += nt * kU) {
+    int64_t b0[kU], b1[kU], c[kU], e[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int64_t s = s0 + int64_t(u) * nt + threadIdx.x;
+      b0[u] = s < s_hi ? g.crp(s) : 0;
+      b1[u] = s < s_hi ? g.crp(s + 1) : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      c[u] = b1[u] > b0[u] ? static_cast<int64_t>(g.Ccol[b0[u]]) : 0;
+      e[u] = b1[u] > b0[u] ? static_cast<int64_t>(g.Ccol[b1[u] - 1]) : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int64_t s = s0 + int64_t(u) * nt + threadIdx.x;
+      if (s >= s_hi) continue;
+      const int32_t bucket =
+          b1[u] > b0[u] && g.K > 0 ? static_cast<int32_t>(clampi(c[u], 0, g.K - 1) * kOrderBuckets / g.K) : 0;
+      const int64_t span = e[u] > c[u] ? e[u] - c[u] : c[u] - e[u];
+      g.keys[s] = bucket | (span * kOrderLocalDiv < g.K ? kKeyLocal : 0);
+    }
+  }
+}
+
+// One work-group (up to 1024 threads); cnt: kOrderBuckets int32 of LDS,
+// part: one int32 of LDS per thread.
+template <typename I>
+__device__ void sort_windows(const Geometry<I>& g, int32_t* cnt, int32_t* part) {
   const int tid = threadIdx.x, nt = blockDim.x;
   __shared__ int32_t s_local;
-  auto bucket = [&](int64_t b0, int64_t b1, int64_t c) -> int {
-    if (b1 <= b0 || g.K <= 0) return 0;
-    return static_cast<int>(clampi(c, 0, g.K - 1) * kOrderBuckets / g.K);
-  };
   for (int i = tid; i < kOrderBuckets; i += nt) cnt[i] = 0;
   if (tid == 0) s_local = 0;
   __syncthreads();
-  constexpr int kU = 4;  // windows per thread per round, their loads issued together
-  for (int pass = 0; pass < 2; ++pass) {  // 0: histogram; 1: scatter (keys recomputed)
-    int32_t local = 0;
-    for (int64_t s0 = 0; s0 < g.cwin; s0 += int64_t(nt) * kU) {
-      int64_t b0[kU], b1[kU], c[kU], e[kU];
+  constexpr int kU = 8;  // keys per thread per round, their loads issued together
+  int32_t local = 0;
+  for (int64_t s0 = 0; s0 < g.cwin; s0 += int64_t(nt) * kU) {
+    int32_t k[kU];
 #pragma unroll
-      for (int u = 0; u < kU; ++u) {
-        const int64_t s = s0 + int64_t(u) * nt + tid;
-        b0[u] = s < g.cwin ? g.crp(s) : 0;
-        b1[u] = s < g.cwin ? g.crp(s + 1) : 0;
-      }
+    for (int u = 0; u < kU; ++u) {
+      const int64_t s = s0 + int64_t(u) * nt + tid;
+      k[u] = s < g.cwin ? g.keys[s] : -1;
+    }
 #pragma unroll
-      for (int u = 0; u < kU; ++u) {
-        c[u] = b1[u] > b0[u] ? static_cast<int64_t>(g.Ccol[b0[u]]) : 0;
-        e[u] = pass == 0 && b1[u] > b0[u] ? static_cast<int64_t>(g.Ccol[b1[u] - 1]) : 0;
-      }
+    for (int u = 0; u < kU; ++u) {
+      if (k[u] < 0) continue;
+      atomicAdd(&cnt[k[u] & (kKeyLocal - 1)], 1);
+      local += (k[u] & kKeyLocal) ? 1 : 0;
+    }
+  }
+  atomicAdd(&s_local, local);
+  __syncthreads();
+  if (2 * static_cast<int64_t>(s_local) < g.cwin) {  // not local: identity order
+    for (int64_t s = tid; s < g.cwin; s += nt) g.order[s] = static_cast<int32_t>(s);
+    return;
+  }
+  // Exclusive scan of the bucket counts: per-thread runs, then a
+  // Hillis-Steele scan of the run sums.
+  const int per = (kOrderBuckets + nt - 1) / nt;
+  int32_t sum = 0;
+  for (int q = 0; q < per; ++q) {
+    const int i = tid * per + q;
+    if (i < kOrderBuckets) sum += cnt[i];
+  }
+  part[tid] = sum;
+  __syncthreads();
+  for (int off = 1; off < nt; off *= 2) {
+    const int32_t t = tid >= off ? part[tid - off] : 0;
+    __syncthreads();
+    part[tid] += t;
+    __syncthreads();
+  }
+  int32_t run = part[tid] - sum;
+  for (int q = 0; q < per; ++q) {
+    const int i = tid * per + q;
+    if (i < kOrderBuckets) {
+      const int32_t v = cnt[i];
+      cnt[i] = run;
+      run += v;
+    }
+  }
+  __syncthreads();
+  for (int64_t s0 = 0; s0 < g.cwin; s0 += int64_t(nt) * kU) {
+    int32_t k[kU];
 #pragma unroll
-      for (int u = 0; u < kU; ++u) {
-        const int64_t s = s0 + int64_t(u) * nt + tid;
-        if (s >= g.cwin) continue;
-        const int k = bucket(b0[u], b1[u], c[u]);
-        if (pass == 0) {
-          atomicAdd(&cnt[k], 1);
-          const int64_t span = e[u] > c[u] ? e[u] - c[u] : c[u] - e[u];
-          local += span * kOrderLocalDiv < g.K ? 1 : 0;
-        } else {
-          g.order[atomicAdd(&cnt[k], 1)] = static_cast<int32_t>(s);
-        }
-      }
+    for (int u = 0; u < kU; ++u) {
+      const int64_t s = s0 + int64_t(u) * nt + tid;
+      k[u] = s < g.cwin ? g.keys[s] : -1;
     }
-    if (pass == 1) break;
-    atomicAdd(&s_local, local);
-    __syncthreads();
-    if (2 * static_cast<int64_t>(s_local) < g.cwin) {  // not local: identity order
-      for (int64_t s = tid; s < g.cwin; s += nt) g.order[s] = static_cast<int32_t>(s);
-      return;
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      if (k[u] < 0) continue;
+      const int64_t s = s0 + int64_t(u) * nt + tid;
+      g.order[atomicAdd(&cnt[k[u] & (kKeyLocal - 1)], 1)] = static_cast<int32_t>(s);
     }
-    // Exclusive scan of the bucket counts: per-thread runs, then a
-    // Hillis-Steele scan of the run sums (nt <= 1024).
-    const int per = (kOrderBuckets + nt - 1) / nt;
-    int32_t sum = 0;
-    for (int k = 0; k < per; ++k) {
-      const int i = tid * per + k;
-      if (i < kOrderBuckets) sum += cnt[i];
-    }
-    part[tid] = sum;
-    __syncthreads();
-    for (int off = 1; off < nt; off *= 2) {
-      const int32_t t = tid >= off ? part[tid - off] : 0;
-      __syncthreads();
-      part[tid] += t;
-      __syncthreads();
-    }
-    int32_t run = part[tid] - sum;
-    for (int k = 0; k < per; ++k) {
-      const int i = tid * per + k;
-      if (i < kOrderBuckets) {
-        const int32_t v = cnt[i];
-        cnt[i] = run;
-        run += v;
-      }
-    }
-    __syncthreads();
   }
 }
 
@@ -482,15 +524,11 @@ __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM
   // wg_split > 1 each XCD's L2 serves one column chunk of the dense rows.
   // With a window order to write (kOrder: a separate instantiation, so the
   // plain gather keeps its register budget), work-groups [0, kXcds) come
-  // first: the first one sorts the windows while the gathers run, the others
-  // exit.
+  // first and write the windows' sort keys while the gathers run.
   int64_t bid = static_cast<int64_t>(blockIdx.x);
   if constexpr (kOrder) {
     if (bid < kXcds) {
-      if (bid == 0) {
-        int32_t* ord = reinterpret_cast<int32_t*>(smem);
-        order_windows(g, ord, ord + kOrderBuckets);
-      }
+      window_keys(g, bid);
       return;
     }
     bid -= kXcds;
@@ -645,6 +683,9 @@ __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM
 }
 
 // Post pass, one launch:
+//  * with a window order to write (g.order), work-group 0 sorts the windows
+//    by the keys gather_tiles wrote (LDS: kOrderBuckets + blockDim.x int32),
+//    and the classes below follow from work-group 1;
 //  * work-groups [0, fix_blocks): add the partials of every row that crosses
 //    range ends, in range order (lane group per (range, column chunk));
 //  * the next zero_blocks: zero the block kernel's window counters (mixed
@@ -657,14 +698,24 @@ __global__ __launch_bounds__(kWgThreads) void gather_post(Geometry<I> g, int64_t
                                                           int64_t chunks, int64_t slot, int64_t fix_blocks,
                                                           uint32_t* zero_counts, int64_t count, int64_t zero_blocks) {
   constexpr int V = LaneVec<T>::V;
-  if (static_cast<int64_t>(blockIdx.x) >= fix_blocks && static_cast<int64_t>(blockIdx.x) < fix_blocks + zero_blocks) {
-    const int64_t i = (static_cast<int64_t>(blockIdx.x) - fix_blocks) * blockDim.x + threadIdx.x;
+  int64_t bid = static_cast<int64_t>(blockIdx.x);
+  if (g.order != nullptr) {
+    if (bid == 0) {
+      extern __shared__ __align__(16) unsigned char smem[];
+      int32_t* cnt = reinterpret_cast<int32_t*>(smem);
+      sort_windows(g, cnt, cnt + kOrderBuckets);
+      return;
+    }
+    --bid;
+  }
+  if (bid >= fix_blocks && bid < fix_blocks + zero_blocks) {
+    const int64_t i = (bid - fix_blocks) * blockDim.x + threadIdx.x;
     if (i < count) zero_counts[i] = 0u;
     return;
   }
-  if (static_cast<int64_t>(blockIdx.x) < fix_blocks) {
+  if (bid < fix_blocks) {
     const int L = 1 << log2L;
-    const int64_t tid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int64_t tid = bid * blockDim.x + threadIdx.x;
     const int64_t item = tid >> log2L;
     const int lane = static_cast<int>(tid & (L - 1));
     if (item >= (g.nranges - 1) * chunks) return;
@@ -717,7 +768,7 @@ __global__ __launch_bounds__(kWgThreads) void gather_post(Geometry<I> g, int64_t
   // Empty rows: wavefront w takes rows [row_lo + 64w, +64).
   const int lane = threadIdx.x & 63;
   const int64_t wave =
-      (static_cast<int64_t>(blockIdx.x) - fix_blocks - zero_blocks) * (blockDim.x >> 6) + (threadIdx.x >> 6);
+      (bid - fix_blocks - zero_blocks) * (blockDim.x >> 6) + (threadIdx.x >> 6);
   const int64_t r = g.row_lo + wave * 64 + lane;
   // Rows of block windows with blocks are written by the block kernel.
   const bool zero_row = r < g.row_hi && g.rp(r) == g.rp(r + 1) && !g.in_block_window(r);
@@ -876,7 +927,9 @@ spmm_status gather_typed(const void* rowptr, const void* col, const void* value,
   g.vpart = vpart;
   g.Ccol = static_cast<const I*>(Ccol);
   g.K = K;
+  // `order` holds 2 * cwin int32: the order, then the windows' keys.
   g.order = Crowptr && cwin > 0 && cwin <= kOrderMaxWindows && nnz > 0 ? order : nullptr;
+  g.keys = g.order != nullptr ? g.order + cwin : nullptr;
 
   if (K > static_cast<int64_t>(kBadCol) - 1)
     return fail(SPMM_ERR_CONTRACT, "dense has too many rows for 32-bit column ids");
@@ -917,7 +970,6 @@ spmm_status gather_typed(const void* rowptr, const void* col, const void* value,
   if (g.nnz > 0) {
     const int64_t tiles = ceil_div(g.nranges, ranges_per_tile);
     size_t lds = static_cast<size_t>((ranges_per_tile + 1) * g.range) * Staged<T>::bytes_per_position();
-    if (g.order && lds < (kOrderBuckets + 1024) * sizeof(int32_t)) lds = (kOrderBuckets + 1024) * sizeof(int32_t);
     // Dense operands within a 32-bit byte extent use buffer loads.
     const bool buffer = buffer_extent(K, ld, N, sizeof(T)) <= kBufferLimit;
     auto kernel = g.order ? (buffer ? gather_tiles<T, I, BufferLoader<T>, true> : gather_tiles<T, I, GlobalLoader<T>, true>)
@@ -937,8 +989,11 @@ spmm_status gather_typed(const void* rowptr, const void* col, const void* value,
   const int64_t fix_blocks = ceil_div(fix_items, kWgThreads);
   const int64_t row_blocks = ceil_div(ceil_div(row_hi - row_lo, 64), kWgThreads / 64);
   const int64_t zero_blocks = zero_counts != nullptr ? ceil_div(count, kWgThreads) : 0;
-  hipLaunchKernelGGL((gather_post<T, I>), dim3(static_cast<unsigned>(fix_blocks + zero_blocks + row_blocks)),
-                     dim3(kWgThreads), 0, stream, g, N, ld, static_cast<T*>(out),
+  const int64_t order_blocks = g.order != nullptr ? 1 : 0;
+  const size_t post_lds = g.order != nullptr ? (kOrderBuckets + kWgThreads) * sizeof(int32_t) : 0;
+  hipLaunchKernelGGL((gather_post<T, I>),
+                     dim3(static_cast<unsigned>(order_blocks + fix_blocks + zero_blocks + row_blocks)),
+                     dim3(kWgThreads), post_lds, stream, g, N, ld, static_cast<T*>(out),
                      static_cast<const float*>(partial), log2L, chunks, slot, fix_blocks, zero_counts, count,
                      zero_blocks);
   return check_launch("gather_post");

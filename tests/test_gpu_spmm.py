@@ -175,11 +175,11 @@ def test_block_path_width_invariant_bitwise(spmm_npu, dtype):
 @pytest.mark.parametrize("dtype", ["fp16", "fp32"])
 def test_block_window_order_on_a_banded_layout(spmm_npu, dtype):
     """The preprocess layout of a banded matrix (windows sorted by density,
-    each spanning a narrow band of columns) with dense rows of 512 bytes or
+    each spanning a narrow band of columns) with dense rows of 256 bytes or
     more takes the block windows' locality order.  The order changes only
     which work-group runs first, so the result equals a narrower run without
-    the order (fp16 N=128, fp32 N=64) bit for bit on its columns, and the
-    restored rows match A @ B."""
+    the order (128-byte rows: fp16 N=64, fp32 N=32) bit for bit on its
+    columns, and the restored rows match A @ B."""
     rng = np.random.default_rng(97)
     rows, band = 3000, 48
     deg = rng.integers(0, 2 * band, rows)
@@ -204,9 +204,9 @@ def test_block_window_order_on_a_banded_layout(spmm_npu, dtype):
             dev(Bn), dev(O.make_start(p["crow_window_ptr"].numpy(), 20)),
             dev(O.make_start(p["vrow_window_ptr"].numpy(), 40)))
 
-    narrow = 128 if dtype == "fp16" else 64  # dense rows under 512 bytes: no order
+    narrow = 64 if dtype == "fp16" else 32  # dense rows under 256 bytes: no order
     base = run(np.ascontiguousarray(B[:, :narrow])).cpu()
-    for n in (256, 512):
+    for n in (128, 256, 512):
         out = run(np.ascontiguousarray(B[:, :n]))
         assert torch.equal(out[:, :narrow].cpu(), base), f"width {n} differs from {narrow}"
         got = spmm_npu.restore_node_tensor(out, p["inv_permutation"].cuda())[:rows]
@@ -228,6 +228,42 @@ def test_mixed_with_empty_block_part_equals_csr_bitwise(spmm_npu, dtype, width):
         dev(crow, i32), dev(col, i32), dev(vals), dev(B), zero_start(20),
         dev(O.make_start(crow, 40)))
     assert torch.equal(mixed[:333].cpu(), ref.cpu())
+
+
+@pytest.mark.parametrize("windows", [16384, 16385])
+def test_window_order_at_its_limit(spmm_npu, windows):
+    """Block part of a banded matrix (csr_to_bcsr: every window local) plus
+    a random vector part, so the gather kernel runs beside it: with 16384
+    windows (the most the locality order takes) the sort's key and scatter
+    loops make several rounds; with 16385 the windows keep their order.  The
+    result matches A1 @ B + A2 @ B in fp64, and at N=128 (ordered when
+    16384) equals N=64 (never ordered) bit for bit on its columns."""
+    rng = np.random.default_rng(61)
+    rows = 16 * windows
+    deg = rng.integers(2, 9, rows)
+    lo = np.maximum(np.arange(rows) - 8, 0)
+    parts = [np.sort(rng.choice(np.arange(lo[r], min(rows, lo[r] + 16)), int(deg[r]), replace=False))
+             for r in range(rows)]
+    crow = np.zeros(rows + 1, np.int64)
+    crow[1:] = np.cumsum([p.size for p in parts])
+    col = np.concatenate(parts).astype(np.int64)
+    vals = rng.uniform(-1, 1, col.size).astype(np.float16)
+    vcrow, vcol = random_csr(rng, rows, rows, 2, empty_frac=0.5)
+    vvals = rng.uniform(-1, 1, vcol.size).astype(np.float16)
+    b = O.csr_to_bcsr(crow, col, vals, rows, rows, 16)
+    assert b["crow_window_ptr"].size - 1 == windows
+    B = rng.standard_normal((rows, 128)).astype(np.float16)
+    i32 = torch.int32
+
+    def run(n):
+        return spmm_npu.spmm_ascend_cube(
+            dev(b["crow_window_ptr"], i32), dev(b["unique_col_ids"], i32), dev(b["value"]),
+            dev(vcrow, i32), dev(vcol, i32), dev(vvals), dev(np.ascontiguousarray(B[:, :n])),
+            dev(O.make_start(b["crow_window_ptr"], 20)), dev(O.make_start(vcrow, 40)))
+
+    out = run(128)
+    assert_close(out[:rows], O.spmm_f64(crow, col, vals, B) + O.spmm_f64(vcrow, vcol, vvals, B), "fp16")
+    assert torch.equal(out[:, :64].cpu(), run(64).cpu())
 
 
 @pytest.mark.parametrize("dtype", ["fp16", "fp32"])
