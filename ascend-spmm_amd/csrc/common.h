@@ -100,12 +100,11 @@ spmm_status launch_gather(int32_t index_type, int32_t value_type,
                           const void* Ccol, int32_t* order, uint32_t* zero_counts, int64_t count,
                           hipStream_t stream);
 
-// Locality order of the block windows: with `order` set (2 * cwin int32:
-// the order, then one sort key per window), extra work-groups of the gather
-// kernel, running beside the gathers, write each window's key (its first
-// block column's bucket of kOrderBuckets, and whether the window is local),
-// the post pass's first work-group sorts the windows by key, and the block
-// kernel follows that order.  Used for at most kOrderMaxWindows windows,
+// Locality order of the block windows: with `order` set (order_words(cwin)
+// int32), extra work-groups of the gather kernel, running beside the
+// gathers, bucket the windows by first block column (kOrderBuckets buckets)
+// in kXcds shares, the post pass's first work-groups scatter each share into
+// the order, and the block kernel follows that order.  Used for at most kOrderMaxWindows windows,
 // dense rows of at least kOrderMinRowBytes (fp16 N >= 128, fp32 N >= 64),
 // and a vector part (the gather kernel runs).
 constexpr int64_t kOrderMaxWindows = 16384;
@@ -121,6 +120,10 @@ constexpr int64_t kOrderMinRowBytes = SPMM_ORDER_MIN_ROW_BYTES;
 #define SPMM_BLOCK_XCD_RUN 32
 #endif
 constexpr int64_t kBlockXcdRun = SPMM_BLOCK_XCD_RUN;
+
+// int32 words of the order workspace for `windows` windows: the order, one
+// key per window, a histogram per XCD share and a local-window count per share.
+inline int64_t order_words(int64_t windows) { return 2 * windows + kXcds * (kOrderBuckets + 1); }
 
 inline bool block_order_wanted(int64_t windows, int64_t vector_nnz, int64_t width, int32_t value_type) {
   const int64_t row_bytes = width * (value_type == SPMM_VALUE_F16 ? 2 : 4);

@@ -253,9 +253,9 @@ struct MixedLayout {
     ranges = block_overflow_ranges(limit, block_chunk_for(d->value_type, limit));
     slots = align_up(static_cast<size_t>(ranges * 2 * 16) * w * sizeof(float) +
                          static_cast<size_t>(ranges) * sizeof(uint32_t), 256);
-    // The block windows' locality order and their sort keys (block_order_wanted).
+    // The block windows' locality order and its sort state (block_order_wanted).
     order = block_order_wanted(d->block_windows, d->vector_nnz, w, d->value_type)
-                ? align_up(static_cast<size_t>(2 * d->block_windows) * sizeof(int32_t), 256)
+                ? align_up(static_cast<size_t>(order_words(d->block_windows)) * sizeof(int32_t), 256)
                 : 0;
   }
   size_t total() const { return gather + vpart + slots + order; }

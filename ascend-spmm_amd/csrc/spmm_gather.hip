@@ -106,13 +106,16 @@ struct Geometry {
   const I* Crowptr;
   int64_t cwin, climit;
   float* vpart;
-  // Locality order of the block windows when set: gather_tiles' extra
-  // work-groups write one key per window (keys, cwin entries), gather_post's
-  // first work-group sorts the windows by key into order (cwin entries).
+  // Locality order of the block windows when set (order_words(cwin) int32
+  // from `order`): gather_tiles' extra work-groups write one key per window
+  // and one bucket histogram per share of the windows, gather_post's first
+  // work-groups scatter the windows into the order.
   const I* Ccol;
   int64_t K;
-  int32_t* order;
-  int32_t* keys;
+  int32_t* order;   // [cwin]: the order
+  int32_t* keys;    // [cwin]: bucket | rank within the share's bucket << kKeyRankShift
+  int32_t* hist;    // [kXcds][kOrderBuckets]: windows per bucket of each share
+  int32_t* nlocal;  // [kXcds]: local windows of each share
 
   __device__ inline int64_t rp(int64_t r) const {
     return clampi(static_cast<int64_t>(rowptr[r < vrows ? r : vrows]), 0, nnz);
@@ -370,33 +373,44 @@ __device__ inline int64_t find_row(const Geometry<I>& g, int64_t P) {
 // gather the same dense rows end up next to each other, and the block kernel
 // deals runs of consecutive positions of the order to the XCDs in turn, so
 // the XCDs sweep the dense operand together and each XCD's L2 holds the rows
-// its next windows need.  Any permutation
-// gives the same results (every window is summed by its own work-group), so
-// ties within a bucket take the order of the LDS atomics.
+// its next windows need.  Any permutation gives the same results (every
+// window is summed by its own work-group), so ties within a bucket take the
+// order of the LDS atomics.
 //
 // The order only pays where windows are local (their block columns span a
 // small part of [0, K), as in banded or clustered matrices).  When fewer than
 // half the windows span less than K / kOrderLocalDiv columns, the identity
 // order is written instead.
 //
-// Two steps, so that neither sits on the critical path of its kernel:
+// The windows are cut into kXcds shares; two steps, so that neither sits on
+// the critical path of its kernel:
 //  * window_keys, in gather_tiles' kXcds extra work-groups beside the
-//    gathers: each work-group reads the block range and the first and last
-//    block column of its share of the windows (two dependent rounds of
-//    loads) and writes key = bucket | kKeyLocal when the window is local;
-//  * sort_windows, in gather_post's first work-group: a histogram of the
-//    keys in LDS, a scan, and the scatter into the order (the keys, 4 bytes
-//    per window, are read twice, from L2).
+//    gathers, one per share: read each window's block range and first and
+//    last block column (two dependent rounds of loads), count the share's
+//    windows per bucket in LDS (the count before a window is its rank in
+//    the bucket), and write key = bucket | rank << kKeyRankShift per window,
+//    the share's histogram, and its number of local windows;
+//  * scatter_share, in gather_post's first kXcds work-groups, one per share:
+//    read the kXcds histograms, scan them into the share's start in every
+//    bucket, and write each window of the share to start[bucket] + rank.
 constexpr int64_t kOrderLocalDiv = 8;
-constexpr int32_t kKeyLocal = 1 << 20;
-static_assert(kOrderBuckets < kKeyLocal, "bucket ids fit below the local bit");
+constexpr int kKeyRankShift = 10;
+static_assert(kOrderBuckets <= (1 << kKeyRankShift), "bucket ids fit below the rank");
+static_assert((kOrderMaxWindows + kXcds - 1) / kXcds < (int64_t(1) << (31 - kKeyRankShift)),
+              "ranks within a share fit the key");
 
+// One work-group; hist: kOrderBuckets int32 of LDS.
 template <typename I>
-__device__ void window_keys(const Geometry<I>& g, int64_t part) {
+__device__ void window_keys(const Geometry<I>& g, int64_t part, int32_t* hist) {
   const int64_t share = (g.cwin + kXcds - 1) / kXcds;
   const int64_t s_lo = part * share;
   const int64_t s_hi = s_lo + share < g.cwin ? s_lo + share : g.cwin;
   const int64_t nt = blockDim.x;
+  __shared__ int32_t s_local;
+  for (int64_t i = threadIdx.x; i < kOrderBuckets; i += nt) hist[i] = 0;
+  if (threadIdx.x == 0) s_local = 0;
+  __syncthreads();
+  int32_t local = 0;
   constexpr int kU = 4;  // windows per thread per round, their loads issued together
   for (int64_t s0 = s_lo; s0 < s_hi; s0 += nt * kU) {
     int64_t b0[kU], b1[kU], c[kU], e[kU];
@@ -418,80 +432,93 @@ __device__ void window_keys(const Geometry<I>& g, int64_t part) {
       const int32_t bucket =
           b1[u] > b0[u] && g.K > 0 ? static_cast<int32_t>(clampi(c[u], 0, g.K - 1) * kOrderBuckets / g.K) : 0;
       const int64_t span = e[u] > c[u] ? e[u] - c[u] : c[u] - e[u];
-      g.keys[s] = bucket | (span * kOrderLocalDiv < g.K ? kKeyLocal : 0);
-    }
-  }
-}
-
-// One work-group (up to 1024 threads); cnt: kOrderBuckets int32 of LDS,
-// part: one int32 of LDS per thread.
-template <typename I>
-__device__ void sort_windows(const Geometry<I>& g, int32_t* cnt, int32_t* part) {
-  const int tid = threadIdx.x, nt = blockDim.x;
-  __shared__ int32_t s_local;
-  for (int i = tid; i < kOrderBuckets; i += nt) cnt[i] = 0;
-  if (tid == 0) s_local = 0;
-  __syncthreads();
-  constexpr int kU = 8;  // keys per thread per round, their loads issued together
-  int32_t local = 0;
-  for (int64_t s0 = 0; s0 < g.cwin; s0 += int64_t(nt) * kU) {
-    int32_t k[kU];
-#pragma unroll
-    for (int u = 0; u < kU; ++u) {
-      const int64_t s = s0 + int64_t(u) * nt + tid;
-      k[u] = s < g.cwin ? g.keys[s] : -1;
-    }
-#pragma unroll
-    for (int u = 0; u < kU; ++u) {
-      if (k[u] < 0) continue;
-      atomicAdd(&cnt[k[u] & (kKeyLocal - 1)], 1);
-      local += (k[u] & kKeyLocal) ? 1 : 0;
+      local += span * kOrderLocalDiv < g.K ? 1 : 0;
+      g.keys[s] = bucket | (atomicAdd(&hist[bucket], 1) << kKeyRankShift);
     }
   }
   atomicAdd(&s_local, local);
   __syncthreads();
-  if (2 * static_cast<int64_t>(s_local) < g.cwin) {  // not local: identity order
-    for (int64_t s = tid; s < g.cwin; s += nt) g.order[s] = static_cast<int32_t>(s);
+  for (int64_t i = threadIdx.x; i < kOrderBuckets; i += nt) g.hist[part * kOrderBuckets + i] = hist[i];
+  if (threadIdx.x == 0) g.nlocal[part] = s_local;
+}
+
+// One work-group of kWgThreads threads; start: kOrderBuckets int32 of LDS,
+// run: kWgThreads int32 of LDS.
+template <typename I>
+__device__ void scatter_share(const Geometry<I>& g, int64_t part, int32_t* start, int32_t* run) {
+  const int tid = threadIdx.x, nt = blockDim.x;
+  const int64_t share = (g.cwin + kXcds - 1) / kXcds;
+  const int64_t s_lo = part * share;
+  const int64_t s_hi = s_lo + share < g.cwin ? s_lo + share : g.cwin;
+  int64_t local = 0;
+#pragma unroll
+  for (int b = 0; b < kXcds; ++b) local += g.nlocal[b];
+  if (2 * local < g.cwin) {  // not local: identity order
+    for (int64_t s = s_lo + tid; s < s_hi; s += nt) g.order[s] = static_cast<int32_t>(s);
     return;
   }
-  // Exclusive scan of the bucket counts: per-thread runs, then a
-  // Hillis-Steele scan of the run sums.
-  const int per = (kOrderBuckets + nt - 1) / nt;
+  // Thread tid takes buckets [tid * kPer, (tid + 1) * kPer): their totals
+  // over the shares, and the windows of the shares before this one, which
+  // is this share's offset inside each bucket.
+  constexpr int kPer = (kOrderBuckets + kWgThreads - 1) / kWgThreads;
+  int32_t tot[kPer];
   int32_t sum = 0;
-  for (int q = 0; q < per; ++q) {
-    const int i = tid * per + q;
-    if (i < kOrderBuckets) sum += cnt[i];
+  {
+    int32_t h[kXcds][kPer];
+#pragma unroll
+    for (int b = 0; b < kXcds; ++b)
+#pragma unroll
+      for (int q = 0; q < kPer; ++q) {
+        const int k = tid * kPer + q;
+        h[b][q] = k < kOrderBuckets ? g.hist[b * kOrderBuckets + k] : 0;
+      }
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) {
+      int32_t pre = 0;
+      tot[q] = 0;
+#pragma unroll
+      for (int b = 0; b < kXcds; ++b) {
+        tot[q] += h[b][q];
+        pre += b < part ? h[b][q] : 0;
+      }
+      const int k = tid * kPer + q;
+      if (k < kOrderBuckets) start[k] = pre;
+      sum += tot[q];
+    }
   }
-  part[tid] = sum;
+  // Exclusive scan of the per-thread bucket totals (inclusive Hillis-Steele
+  // scan, minus the own sum), then each bucket's start.
+  run[tid] = sum;
   __syncthreads();
   for (int off = 1; off < nt; off *= 2) {
-    const int32_t t = tid >= off ? part[tid - off] : 0;
+    const int32_t t = tid >= off ? run[tid - off] : 0;
     __syncthreads();
-    part[tid] += t;
+    run[tid] += t;
     __syncthreads();
   }
-  int32_t run = part[tid] - sum;
-  for (int q = 0; q < per; ++q) {
-    const int i = tid * per + q;
-    if (i < kOrderBuckets) {
-      const int32_t v = cnt[i];
-      cnt[i] = run;
-      run += v;
+  int32_t at = run[tid] - sum;
+#pragma unroll
+  for (int q = 0; q < kPer; ++q) {
+    const int k = tid * kPer + q;
+    if (k < kOrderBuckets) {
+      start[k] += at;
+      at += tot[q];
     }
   }
   __syncthreads();
-  for (int64_t s0 = 0; s0 < g.cwin; s0 += int64_t(nt) * kU) {
-    int32_t k[kU];
+  constexpr int kU = 8;  // keys per thread per round, their loads issued together
+  for (int64_t s0 = s_lo; s0 < s_hi; s0 += int64_t(nt) * kU) {
+    int32_t key[kU];
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
       const int64_t s = s0 + int64_t(u) * nt + tid;
-      k[u] = s < g.cwin ? g.keys[s] : -1;
+      key[u] = s < s_hi ? g.keys[s] : -1;
     }
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
-      if (k[u] < 0) continue;
+      if (key[u] < 0) continue;
       const int64_t s = s0 + int64_t(u) * nt + tid;
-      g.order[atomicAdd(&cnt[k[u] & (kKeyLocal - 1)], 1)] = static_cast<int32_t>(s);
+      g.order[start[key[u] & ((1 << kKeyRankShift) - 1)] + (key[u] >> kKeyRankShift)] = static_cast<int32_t>(s);
     }
   }
 }
@@ -528,7 +555,7 @@ __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM
   int64_t bid = static_cast<int64_t>(blockIdx.x);
   if constexpr (kOrder) {
     if (bid < kXcds) {
-      window_keys(g, bid);
+      window_keys(g, bid, reinterpret_cast<int32_t*>(smem));
       return;
     }
     bid -= kXcds;
@@ -683,9 +710,9 @@ __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM
 }
 
 // Post pass, one launch:
-//  * with a window order to write (g.order), work-group 0 sorts the windows
-//    by the keys gather_tiles wrote (LDS: kOrderBuckets + blockDim.x int32),
-//    and the classes below follow from work-group 1;
+//  * with a window order to write (g.order), work-groups [0, kXcds) scatter
+//    one share of the windows each into the order (scatter_share; LDS:
+//    kOrderBuckets + kWgThreads int32), and the classes below follow;
 //  * work-groups [0, fix_blocks): add the partials of every row that crosses
 //    range ends, in range order (lane group per (range, column chunk));
 //  * the next zero_blocks: zero the block kernel's window counters (mixed
@@ -700,13 +727,13 @@ __global__ __launch_bounds__(kWgThreads) void gather_post(Geometry<I> g, int64_t
   constexpr int V = LaneVec<T>::V;
   int64_t bid = static_cast<int64_t>(blockIdx.x);
   if (g.order != nullptr) {
-    if (bid == 0) {
+    if (bid < kXcds) {
       extern __shared__ __align__(16) unsigned char smem[];
-      int32_t* cnt = reinterpret_cast<int32_t*>(smem);
-      sort_windows(g, cnt, cnt + kOrderBuckets);
+      int32_t* start = reinterpret_cast<int32_t*>(smem);
+      scatter_share(g, bid, start, start + kOrderBuckets);
       return;
     }
-    --bid;
+    bid -= kXcds;
   }
   if (bid >= fix_blocks && bid < fix_blocks + zero_blocks) {
     const int64_t i = (bid - fix_blocks) * blockDim.x + threadIdx.x;
@@ -927,9 +954,12 @@ spmm_status gather_typed(const void* rowptr, const void* col, const void* value,
   g.vpart = vpart;
   g.Ccol = static_cast<const I*>(Ccol);
   g.K = K;
-  // `order` holds 2 * cwin int32: the order, then the windows' keys.
+  // `order` holds order_words(cwin) int32: the order, the windows' keys, the
+  // shares' histograms and local-window counts.
   g.order = Crowptr && cwin > 0 && cwin <= kOrderMaxWindows && nnz > 0 ? order : nullptr;
   g.keys = g.order != nullptr ? g.order + cwin : nullptr;
+  g.hist = g.order != nullptr ? g.keys + cwin : nullptr;
+  g.nlocal = g.order != nullptr ? g.hist + kXcds * kOrderBuckets : nullptr;
 
   if (K > static_cast<int64_t>(kBadCol) - 1)
     return fail(SPMM_ERR_CONTRACT, "dense has too many rows for 32-bit column ids");
@@ -970,6 +1000,7 @@ spmm_status gather_typed(const void* rowptr, const void* col, const void* value,
   if (g.nnz > 0) {
     const int64_t tiles = ceil_div(g.nranges, ranges_per_tile);
     size_t lds = static_cast<size_t>((ranges_per_tile + 1) * g.range) * Staged<T>::bytes_per_position();
+    if (g.order && lds < kOrderBuckets * sizeof(int32_t)) lds = kOrderBuckets * sizeof(int32_t);  // window_keys' histogram
     // Dense operands within a 32-bit byte extent use buffer loads.
     const bool buffer = buffer_extent(K, ld, N, sizeof(T)) <= kBufferLimit;
     auto kernel = g.order ? (buffer ? gather_tiles<T, I, BufferLoader<T>, true> : gather_tiles<T, I, GlobalLoader<T>, true>)
@@ -989,7 +1020,7 @@ spmm_status gather_typed(const void* rowptr, const void* col, const void* value,
   const int64_t fix_blocks = ceil_div(fix_items, kWgThreads);
   const int64_t row_blocks = ceil_div(ceil_div(row_hi - row_lo, 64), kWgThreads / 64);
   const int64_t zero_blocks = zero_counts != nullptr ? ceil_div(count, kWgThreads) : 0;
-  const int64_t order_blocks = g.order != nullptr ? 1 : 0;
+  const int64_t order_blocks = g.order != nullptr ? kXcds : 0;
   const size_t post_lds = g.order != nullptr ? (kOrderBuckets + kWgThreads) * sizeof(int32_t) : 0;
   hipLaunchKernelGGL((gather_post<T, I>),
                      dim3(static_cast<unsigned>(order_blocks + fix_blocks + zero_blocks + row_blocks)),

@@ -182,6 +182,65 @@ def test_mixed_block_only_writes_every_row(lib, vector_rows):
     assert (got[16:32] == 0).all() and (got[64:] == 0).all()
 
 
+def banded_csr(rng, rows, width=16, dmin=2, dmax=8):
+    """Rows of dmin..dmax distinct sorted columns inside a band of `width`
+    columns around the diagonal."""
+    deg = rng.integers(dmin, dmax + 1, rows)
+    pick = np.argsort(rng.random((rows, width)), axis=1)
+    offs = np.sort(np.where(np.arange(width)[None, :] < deg[:, None], pick, width), axis=1)
+    lo = np.clip(np.arange(rows) - width // 2, 0, rows - width)
+    col = (lo[:, None] + offs)[offs < width].astype(np.int64)
+    crow = np.zeros(rows + 1, np.int64)
+    crow[1:] = np.cumsum(deg)
+    return crow, col
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("windows", [1, 9, 1000, 16384])
+def test_window_order_writes_every_window(lib, windows):
+    """Block part of a banded matrix plus a random vector part at N=128 fp16,
+    so the block windows take the locality order when they are local (1000
+    and 16384 windows; 1 and 9 windows span too much of K and keep theirs).
+    The output is pre-filled with NaN and the workspace with 0xFF bytes:
+    every row must be written, whatever the workspace held, and match
+    A1 @ B + A2 @ B."""
+    import torch
+
+    import oracle as O
+
+    rng = np.random.default_rng(12 + windows)
+    rows, N = 16 * windows, 128
+    crow, col = banded_csr(rng, rows)
+    vals = rng.uniform(-1, 1, col.size).astype(np.float16)
+    vdeg = rng.integers(0, 3, rows)
+    vcrow = np.zeros(rows + 1, np.int64)
+    vcrow[1:] = np.cumsum(vdeg)
+    vcol = rng.integers(0, rows, int(vcrow[-1])).astype(np.int64)
+    vvals = rng.uniform(-1, 1, vcol.size).astype(np.float16)
+    B = rng.standard_normal((rows, N)).astype(np.float16)
+    b = O.csr_to_bcsr(crow, col, vals, rows, rows, 16)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    p = lambda x: ctypes.c_void_p(x.data_ptr())
+    i32 = np.int32
+    d = [t(b["crow_window_ptr"].astype(i32)), t(b["unique_col_ids"].astype(i32)), t(b["value"]),
+         t(vcrow.astype(i32)), t(vcol.astype(i32)), t(vvals)]
+    m = MixedDesc(windows, b["unique_col_ids"].size, b["value"].size, rows, vcol.size, rows, N, 0, 0)
+    out = torch.full((lib.spmm_mixed_out_rows(ctypes.byref(m)), N), float("nan"), dtype=torch.float16,
+                     device="cuda")
+    ws_bytes = ctypes.c_size_t(0)
+    assert lib.spmm_mixed_workspace(ctypes.byref(m), ctypes.byref(ws_bytes)) == 0
+    ws = torch.full((max(ws_bytes.value, 1),), 255, dtype=torch.uint8, device="cuda")
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    rc = lib.spmm_mixed_run(ctypes.byref(m), *[p(x) for x in d], p(t(B)), p(out), p(ws),
+                            ctypes.c_size_t(ws_bytes.value), stream)
+    assert rc == 0, lib.spmm_last_error()
+    torch.cuda.synchronize()
+    got = out.cpu().double().numpy()
+    assert not np.isnan(got).any()
+    expected = O.spmm_f64(crow, col, vals, B) + O.spmm_f64(vcrow, vcol, vvals, B)
+    assert np.allclose(got[:rows], expected, atol=2e-2, rtol=2e-2)
+
+
 def test_rowscalar_host_validation(lib):
     d = CsrDesc(10, 5, 10, 24, 0, 0)
     assert lib.spmm_csr_rowscalar_run(ctypes.byref(d), None, None, None, None, None, None) == 4
