@@ -429,9 +429,11 @@ __device__ void window_keys(const Geometry<I>& g, int64_t part, int32_t* hist) {
     for (int u = 0; u < kU; ++u) {
       const int64_t s = s0 + int64_t(u) * nt + threadIdx.x;
       if (s >= s_hi) continue;
-      const int32_t bucket =
-          b1[u] > b0[u] && g.K > 0 ? static_cast<int32_t>(clampi(c[u], 0, g.K - 1) * kOrderBuckets / g.K) : 0;
-      const int64_t span = e[u] > c[u] ? e[u] - c[u] : c[u] - e[u];
+      // Column ids are clamped to [0, K) (an invalid id only adds zeros in
+      // the block kernel), so the span arithmetic cannot overflow.
+      const int64_t first = g.K > 0 ? clampi(c[u], 0, g.K - 1) : 0, last = g.K > 0 ? clampi(e[u], 0, g.K - 1) : 0;
+      const int32_t bucket = b1[u] > b0[u] && g.K > 0 ? static_cast<int32_t>(first * kOrderBuckets / g.K) : 0;
+      const int64_t span = last > first ? last - first : first - last;
       local += span * kOrderLocalDiv < g.K ? 1 : 0;
       g.keys[s] = bucket | (atomicAdd(&hist[bucket], 1) << kKeyRankShift);
     }

@@ -196,14 +196,16 @@ def banded_csr(rng, rows, width=16, dmin=2, dmax=8):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("windows", [1, 9, 1000, 16384])
-def test_window_order_writes_every_window(lib, windows):
+@pytest.mark.parametrize("windows,invalid", [(1, False), (9, False), (1000, False), (1000, True), (16384, False)])
+def test_window_order_writes_every_window(lib, windows, invalid):
     """Block part of a banded matrix plus a random vector part at N=128 fp16,
     so the block windows take the locality order when they are local (1000
     and 16384 windows; 1 and 9 windows span too much of K and keep theirs).
     The output is pre-filled with NaN and the workspace with 0xFF bytes:
     every row must be written, whatever the workspace held, and match
-    A1 @ B + A2 @ B."""
+    A1 @ B + A2 @ B.  With `invalid`, some blocks get column ids -5 or K + 7
+    (first and last blocks of windows included, which the order's keys
+    read): they contribute zero."""
     import torch
 
     import oracle as O
@@ -219,10 +221,27 @@ def test_window_order_writes_every_window(lib, windows):
     vvals = rng.uniform(-1, 1, vcol.size).astype(np.float16)
     B = rng.standard_normal((rows, N)).astype(np.float16)
     b = O.csr_to_bcsr(crow, col, vals, rows, rows, 16)
+    ucol = b["unique_col_ids"].astype(np.int64)
+    if invalid:
+        wp = b["crow_window_ptr"].astype(np.int64)
+        nonempty = np.flatnonzero(np.diff(wp) > 0)
+        bad = np.concatenate([wp[nonempty[::7]], wp[nonempty[3::7] + 1] - 1, rng.choice(ucol.size, 50)])
+        ucol[bad[::2]] = -5
+        ucol[bad[1::2]] = rows + 7
+        # The block part's product without the invalid blocks: its CSR form.
+        wins = np.repeat(np.arange(windows), np.diff(wp))
+        r16 = (16 * wins[:, None] + np.arange(16)[None, :]).reshape(-1)
+        c16 = np.repeat(ucol, 16)
+        v16 = b["value"].reshape(-1)
+        keep = (v16 != 0) & (c16 >= 0) & (c16 < rows)
+        order = np.lexsort((c16[keep], r16[keep]))
+        crow = np.zeros(rows + 1, np.int64)
+        crow[1:] = np.cumsum(np.bincount(r16[keep], minlength=rows))
+        col, vals = c16[keep][order], v16[keep][order]
     t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
     p = lambda x: ctypes.c_void_p(x.data_ptr())
     i32 = np.int32
-    d = [t(b["crow_window_ptr"].astype(i32)), t(b["unique_col_ids"].astype(i32)), t(b["value"]),
+    d = [t(b["crow_window_ptr"].astype(i32)), t(ucol.astype(i32)), t(b["value"]),
          t(vcrow.astype(i32)), t(vcol.astype(i32)), t(vvals)]
     m = MixedDesc(windows, b["unique_col_ids"].size, b["value"].size, rows, vcol.size, rows, N, 0, 0)
     out = torch.full((lib.spmm_mixed_out_rows(ctypes.byref(m)), N), float("nan"), dtype=torch.float16,
