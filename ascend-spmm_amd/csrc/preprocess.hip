@@ -570,10 +570,12 @@ __global__ void task_marginal(TaskState* __restrict__ s, const int64_t* __restri
 
 // Marginal blocks sorted by occupancy descending, first-seen ascending
 // (stable_bucket_sort_by_occupancy_desc, boundary_bucket_sort.h:13-56):
-// key = (16 - occupancy) << 48 | first element.  Other blocks sort last.
+// key = (16 - occupancy) << pbits | first element, where every first element
+// is below 2^pbits.  Other blocks get 16 << pbits and sort last, so the sort
+// needs pbits + 5 key bits.
 __global__ void marginal_keys(const TaskState* __restrict__ s, const int64_t* __restrict__ win_start,
                               const int64_t* __restrict__ blk_first, const int64_t* __restrict__ blk_cnt,
-                              int64_t nb, uint64_t* __restrict__ key, int64_t* __restrict__ id,
+                              int64_t nb, int pbits, uint64_t* __restrict__ key, int64_t* __restrict__ id,
                               int* __restrict__ err) {
   const int64_t bw = s->bwin;
   const int64_t b0 = bw >= 0 ? win_start[bw] : 0, b1 = bw >= 0 ? win_start[bw + 1] : 0;
@@ -583,9 +585,9 @@ __global__ void marginal_keys(const TaskState* __restrict__ s, const int64_t* __
       const int64_t occ = blk_cnt[b];
       if (occ < 1 || occ > 16) atomicOr(err, kBadOccupancy);
       const int64_t o = occ < 1 ? 1 : (occ > 16 ? 16 : occ);
-      key[b] = (static_cast<uint64_t>(16 - o) << 48) | static_cast<uint64_t>(blk_first[b]);
+      key[b] = (static_cast<uint64_t>(16 - o) << pbits) | static_cast<uint64_t>(blk_first[b]);
     } else {
-      key[b] = ~0ull;
+      key[b] = uint64_t(16) << pbits;  // after every marginal block
     }
   }
 }
@@ -1360,8 +1362,11 @@ spmm_status task_plan(const Csr& c, bool graph_layout, void* ws, size_t ws_bytes
   launch(task_init, 1, s, A.st);
   launch_reduce(boundary_search, nwin, s, A.snb, A.snnz, A.pnb, A.pnnz, nwin, c.nnz, &A.st->bpos);
   launch(task_marginal, 1, s, A.st, A.swin, A.snb, A.snnz, A.pnb, A.pnnz, c.nnz);
-  launch(marginal_keys, nb, s, A.st, S.win_start, S.blk_first, S.blk_cnt, nb, A.mkey, A.mid, S.err);
-  if (hipError_t e = x.prims.sort_pairs(A.mkey, A.smkey, A.mid, A.morder, nb, 64))
+  // Keys (16 - occupancy) << pbits | first element (< n <= 2^pbits), and
+  // 16 << pbits for blocks outside the marginal window: pbits + 5 key bits.
+  const int pbits = bits_for(static_cast<uint64_t>(n));
+  launch(marginal_keys, nb, s, A.st, S.win_start, S.blk_first, S.blk_cnt, nb, pbits, A.mkey, A.mid, S.err);
+  if (hipError_t e = x.prims.sort_pairs(A.mkey, A.smkey, A.mid, A.morder, nb, pbits + 5))
     return check_hip(e, "marginal sort");
   launch(marginal_occ, nb + 1, s, A.morder, S.blk_cnt, A.st, nb, A.occ);
   if (hipError_t e = x.prims.exclusive_sum(A.occ, A.assigned, nb + 1)) return check_hip(e, "assigned");
