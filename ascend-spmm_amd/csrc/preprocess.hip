@@ -117,6 +117,12 @@ struct Prims {
   }
 };
 
+// Most blocks the marginal window can hold: distinct columns of one window.
+inline int64_t marginal_capacity(int64_t nb, int64_t ncols) {
+  const int64_t m = nb < ncols ? nb : ncols;
+  return m > 0 ? m : 1;
+}
+
 inline int bits_for(uint64_t max_value) {
   int b = 0;
   while (b < 64 && (max_value >> b) != 0) ++b;
@@ -569,33 +575,36 @@ __global__ void task_marginal(TaskState* __restrict__ s, const int64_t* __restri
 }
 
 // Marginal blocks sorted by occupancy descending, first-seen ascending
-// (stable_bucket_sort_by_occupancy_desc, boundary_bucket_sort.h:13-56):
-// key = (16 - occupancy) << pbits | first element, where every first element
-// is below 2^pbits.  Other blocks get 16 << pbits and sort last, so the sort
-// needs pbits + 5 key bits.
+// (stable_bucket_sort_by_occupancy_desc, boundary_bucket_sort.h:13-56).
+// The marginal window's blocks [b0, b1) are distinct columns of one window,
+// so at most mcap = min(nb, ncols) of them: entry q < mcap is block b0 + q,
+// key = (16 - occupancy) << pbits | first element (every first element is
+// below 2^pbits); entries past b1 get 16 << pbits and sort last, so the sort
+// needs pbits + 5 key bits over mcap entries, not over every block.
 __global__ void marginal_keys(const TaskState* __restrict__ s, const int64_t* __restrict__ win_start,
                               const int64_t* __restrict__ blk_first, const int64_t* __restrict__ blk_cnt,
-                              int64_t nb, int pbits, uint64_t* __restrict__ key, int64_t* __restrict__ id,
+                              int64_t mcap, int pbits, uint64_t* __restrict__ key, int64_t* __restrict__ id,
                               int* __restrict__ err) {
   const int64_t bw = s->bwin;
   const int64_t b0 = bw >= 0 ? win_start[bw] : 0, b1 = bw >= 0 ? win_start[bw + 1] : 0;
-  GRID_STRIDE(b, nb) {
-    id[b] = b;
-    if (b >= b0 && b < b1) {
+  GRID_STRIDE(q, mcap) {
+    const int64_t b = b0 + q;
+    id[q] = b;
+    if (b < b1) {
       const int64_t occ = blk_cnt[b];
       if (occ < 1 || occ > 16) atomicOr(err, kBadOccupancy);
       const int64_t o = occ < 1 ? 1 : (occ > 16 ? 16 : occ);
-      key[b] = (static_cast<uint64_t>(16 - o) << pbits) | static_cast<uint64_t>(blk_first[b]);
+      key[q] = (static_cast<uint64_t>(16 - o) << pbits) | static_cast<uint64_t>(blk_first[b]);
     } else {
-      key[b] = uint64_t(16) << pbits;  // after every marginal block
+      key[q] = uint64_t(16) << pbits;  // after every marginal block
     }
   }
 }
 
 __global__ void marginal_occ(const int64_t* __restrict__ order, const int64_t* __restrict__ blk_cnt,
-                             const TaskState* __restrict__ s, int64_t nb, int64_t* __restrict__ occ) {
+                             const TaskState* __restrict__ s, int64_t mcap, int64_t* __restrict__ occ) {
   const int64_t c = s->bblocks;
-  GRID_STRIDE(q, nb + 1) occ[q] = q < c ? blk_cnt[order[q]] : 0;
+  GRID_STRIDE(q, mcap + 1) occ[q] = q < c ? blk_cnt[order[q]] : 0;
 }
 
 // max(aic, aiv) for the first q marginal blocks on AIC (custom_op.cpp:855-885).
@@ -655,10 +664,14 @@ __global__ void marginal_finish(TaskState* __restrict__ s, const int64_t* __rest
   (void)nwin;
 }
 
-// to_aic per block: the first baic blocks of the marginal order.
+// to_aic per block of the marginal window (the only blocks it is read for):
+// the first baic blocks of the marginal order.
 __global__ void marginal_to_aic(const TaskState* __restrict__ s, const int64_t* __restrict__ order,
-                                int64_t nb, int64_t* __restrict__ to_aic) {
-  GRID_STRIDE(i, nb) to_aic[order[i]] = (s->bwin >= 0 && i < s->baic) ? 1 : 0;
+                                int64_t mcap, int64_t* __restrict__ to_aic) {
+  const int64_t c = s->bwin >= 0 ? s->bblocks : 0;
+  GRID_STRIDE(i, mcap) {
+    if (i < c) to_aic[order[i]] = i < s->baic ? 1 : 0;
+  }
 }
 
 // Window roles: slot (AIC) or AIV rank, in sorted-position order.
@@ -1287,13 +1300,15 @@ struct TaskArrays {
     pnnz = a.take<int64_t>(nwin);
     dkey = a.take<uint64_t>(nwin);
     sdkey = a.take<uint64_t>(nwin);
-    mkey = a.take<uint64_t>(nnz);
-    smkey = a.take<uint64_t>(nnz);
-    mid = a.take<int64_t>(nnz);
-    morder = a.take<int64_t>(nnz);
-    occ = a.take<int64_t>(nnz + 1);
-    assigned = a.take<int64_t>(nnz + 1);
-    to_aic = a.take<int64_t>(nnz);
+    // The marginal window's blocks: at most marginal_capacity(nnz, ncols).
+    const int64_t mcap = marginal_capacity(nnz, c.cols);
+    mkey = a.take<uint64_t>(mcap);
+    smkey = a.take<uint64_t>(mcap);
+    mid = a.take<int64_t>(mcap);
+    morder = a.take<int64_t>(mcap);
+    occ = a.take<int64_t>(mcap + 1);
+    assigned = a.take<int64_t>(mcap + 1);
+    to_aic = a.take<int64_t>(nnz);  // indexed by block
     slot_of = a.take<int64_t>(nwin);
     aiv_win = a.take<int64_t>(nwin);
     aic_win = a.take<int64_t>(nwin);
@@ -1362,18 +1377,19 @@ spmm_status task_plan(const Csr& c, bool graph_layout, void* ws, size_t ws_bytes
   launch(task_init, 1, s, A.st);
   launch_reduce(boundary_search, nwin, s, A.snb, A.snnz, A.pnb, A.pnnz, nwin, c.nnz, &A.st->bpos);
   launch(task_marginal, 1, s, A.st, A.swin, A.snb, A.snnz, A.pnb, A.pnnz, c.nnz);
-  // Keys (16 - occupancy) << pbits | first element (< n <= 2^pbits), and
-  // 16 << pbits for blocks outside the marginal window: pbits + 5 key bits.
+  // The marginal window's blocks (at most mcap), keys (16 - occupancy) <<
+  // pbits | first element (< n <= 2^pbits): pbits + 5 key bits.
   const int pbits = bits_for(static_cast<uint64_t>(n));
-  launch(marginal_keys, nb, s, A.st, S.win_start, S.blk_first, S.blk_cnt, nb, pbits, A.mkey, A.mid, S.err);
-  if (hipError_t e = x.prims.sort_pairs(A.mkey, A.smkey, A.mid, A.morder, nb, pbits + 5))
+  const int64_t mcap = marginal_capacity(nb, c.cols);
+  launch(marginal_keys, mcap, s, A.st, S.win_start, S.blk_first, S.blk_cnt, mcap, pbits, A.mkey, A.mid, S.err);
+  if (hipError_t e = x.prims.sort_pairs(A.mkey, A.smkey, A.mid, A.morder, mcap, pbits + 5))
     return check_hip(e, "marginal sort");
-  launch(marginal_occ, nb + 1, s, A.morder, S.blk_cnt, A.st, nb, A.occ);
-  if (hipError_t e = x.prims.exclusive_sum(A.occ, A.assigned, nb + 1)) return check_hip(e, "assigned");
-  launch_reduce(marginal_min, nb + 1, s, A.st, A.assigned, nb);
-  launch_reduce(marginal_first, nb + 1, s, A.st, A.assigned);
+  launch(marginal_occ, mcap + 1, s, A.morder, S.blk_cnt, A.st, mcap, A.occ);
+  if (hipError_t e = x.prims.exclusive_sum(A.occ, A.assigned, mcap + 1)) return check_hip(e, "assigned");
+  launch_reduce(marginal_min, mcap + 1, s, A.st, A.assigned, mcap);
+  launch_reduce(marginal_first, mcap + 1, s, A.st, A.assigned);
   launch(marginal_finish, 1, s, A.st, A.assigned, nwin);
-  launch(marginal_to_aic, nb, s, A.st, A.morder, nb, A.to_aic);
+  launch(marginal_to_aic, mcap, s, A.st, A.morder, mcap, A.to_aic);
   // Window roles, rows and permutation (custom_op.cpp:887-940).
   launch(window_roles, nwin, s, A.st, A.swin, nwin, A.slot_of, A.aiv_win, A.aic_win);
   launch(aiv_ranks, nwin, s, A.aiv_win, A.st, nwin, A.aiv_rank);
