@@ -190,15 +190,6 @@ __global__ void collect_blocks(const int64_t* __restrict__ bid, int64_t n, const
   }
 }
 
-// Two device scalars gathered for one read-back.
-__global__ void collect_pair(const int64_t* __restrict__ a, const int64_t* __restrict__ b,
-                             int64_t* __restrict__ scal) {
-  if (blockIdx.x == 0 && threadIdx.x == 0) {
-    scal[0] = *a;
-    scal[1] = *b;
-  }
-}
-
 // Expands rows: for element e (position p = p_begin + e) records its row and
 // 64-bit column, checking column range and (optionally) ascending order.
 // Element-parallel, so a row of any length costs the same per element: each
@@ -360,6 +351,34 @@ __global__ void tile_columns(const uint64_t* __restrict__ blk_key, const int64_t
 }
 
 // ------------------------------------------------------- hybrid split
+
+// One key for the block order of the split: occupancy ascending, ties in
+// first-seen order (first element ascending), the order the two stable sorts
+// below give: key = occupancy << pbits | first element (first < 2^pbits).
+// An occupancy of 2^cbits or more (only duplicate CSR entries make one larger
+// than the window) does not fit: *wide is set and the caller takes the
+// two-sort path instead.
+__global__ void split_keys(const int64_t* __restrict__ blk_first, const int64_t* __restrict__ blk_cnt,
+                           int64_t nb, int pbits, int cbits, uint64_t* __restrict__ key,
+                           int64_t* __restrict__ id, int* __restrict__ wide) {
+  const int64_t cmax = (int64_t(1) << cbits) - 1;
+  GRID_STRIDE(b, nb) {
+    const int64_t cnt = blk_cnt[b];
+    if (cnt < 0 || cnt > cmax) atomicOr(wide, 1);
+    const int64_t cc = cnt < 0 ? 0 : (cnt > cmax ? cmax : cnt);
+    key[b] = (static_cast<uint64_t>(cc) << pbits) | static_cast<uint64_t>(blk_first[b]);
+    id[b] = b;
+  }
+}
+
+__global__ void collect_three(const int64_t* __restrict__ a, const int64_t* __restrict__ b,
+                              const int* __restrict__ c, int64_t* __restrict__ scal) {
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    scal[0] = *a;
+    scal[1] = *b;
+    scal[2] = *c;
+  }
+}
 
 // Keys for the first-seen order of blocks (first element = first position).
 __global__ void first_seen_keys(const int64_t* __restrict__ blk_first, int64_t nb,
@@ -1150,8 +1169,10 @@ struct HybridArrays {
   uint64_t *fkey, *fskey, *ckey, *cskey;
   int64_t *fid, *forder, *corder, *cnt_sorted, *prefix, *kept, *kscan, *out_block, *eflag, *vdst;
   unsigned long long* best;  // [2]: min bits, first k
+  int* wide;                 // an occupancy does not fit split_keys' key
   void lay(Arena& a, int64_t rows, int64_t nnz, int64_t W) {
     S.lay(a, rows, nnz, W);
+    wide = a.take<int>(1);
     fkey = a.take<uint64_t>(nnz);
     fskey = a.take<uint64_t>(nnz);
     ckey = a.take<uint64_t>(nnz);
@@ -1178,29 +1199,42 @@ spmm_status hybrid_run(const Csr& c, double a, int64_t W, HybridArrays& H, Ctx& 
   WinSort& S = H.S;
   if (spmm_status st = run_window_sort<I>(c, W, false, S, x)) return st;
   const int64_t nb = S.nb;
-  launch(first_seen_keys, nb, s, S.blk_first, nb, H.fkey, H.fid);
-  if (hipError_t e = x.prims.sort_pairs(H.fkey, H.fskey, H.fid, H.forder, nb,
-                                        bits_for(static_cast<uint64_t>(S.n))))
-    return check_hip(e, "first-seen sort");
-  launch(count_keys, nb, s, H.forder, S.blk_cnt, nb, H.ckey);
-  if (hipError_t e = x.prims.sort_pairs(H.ckey, H.cskey, H.forder, H.corder, nb,
-                                        bits_for(static_cast<uint64_t>(S.n))))
-    return check_hip(e, "count sort");
-  launch(gather_counts, nb + 1, s, H.corder, S.blk_cnt, nb, H.cnt_sorted);
-  if (hipError_t e = x.prims.exclusive_sum(H.cnt_sorted, H.prefix, nb + 1)) return check_hip(e, "prefix");
-  launch(fill_kernel<unsigned long long>, 2, s, H.best, int64_t(2), ~0ull);
-  launch_reduce(split_min, nb + 1, s, H.prefix, nb, a, H.best);
-  launch_reduce(split_first, nb + 1, s, H.prefix, nb, a, H.best, H.best + 1);
-  launch(mark_moved, nb, s, H.corder, nb, H.best, H.best + 1, H.kept);
-  launch(fill_kernel<int64_t>, 1, s, H.kept + nb, int64_t(1), int64_t(0));
-  if (hipError_t e = x.prims.exclusive_sum(H.kept, H.kscan, nb + 1)) return check_hip(e, "kept scan");
-  launch(kept_index, nb, s, H.kept, H.kscan, nb, H.out_block);
-  launch(moved_elements, S.n + 1, s, S.elem_block, H.kept, S.n, H.eflag);
-  if (hipError_t e = x.prims.exclusive_sum(H.eflag, H.vdst, S.n + 1)) return check_hip(e, "residual scan");
-  if (spmm_status st = check_launch("hybrid split")) return st;
-  hipLaunchKernelGGL(collect_pair, dim3(1), dim3(64), 0, s, H.kscan + nb, H.vdst + S.n, S.scal);
-  int64_t v[2] = {0, 0};
-  if (spmm_status st = read_back(v, S.scal, 2, s)) return st;
+  // Block order: one sort on split_keys (occupancy, then first element),
+  // unless an occupancy needs more than cbits; then (second round) the
+  // first-seen sort followed by the stable occupancy sort.
+  const int pbits = bits_for(static_cast<uint64_t>(S.n));
+  const int cbits = bits_for(static_cast<uint64_t>(W > 0 ? W : 1));
+  int64_t v[3] = {0, 0, 0};
+  for (int round = 0; round < 2; ++round) {
+    if (round == 0) {
+      launch(fill_kernel<int>, 1, s, H.wide, int64_t(1), 0);
+      launch(split_keys, nb, s, S.blk_first, S.blk_cnt, nb, pbits, cbits, H.ckey, H.fid, H.wide);
+      if (hipError_t e = x.prims.sort_pairs(H.ckey, H.cskey, H.fid, H.corder, nb, pbits + cbits))
+        return check_hip(e, "block order sort");
+    } else {
+      launch(first_seen_keys, nb, s, S.blk_first, nb, H.fkey, H.fid);
+      if (hipError_t e = x.prims.sort_pairs(H.fkey, H.fskey, H.fid, H.forder, nb, pbits))
+        return check_hip(e, "first-seen sort");
+      launch(count_keys, nb, s, H.forder, S.blk_cnt, nb, H.ckey);
+      if (hipError_t e = x.prims.sort_pairs(H.ckey, H.cskey, H.forder, H.corder, nb, pbits))
+        return check_hip(e, "count sort");
+    }
+    launch(gather_counts, nb + 1, s, H.corder, S.blk_cnt, nb, H.cnt_sorted);
+    if (hipError_t e = x.prims.exclusive_sum(H.cnt_sorted, H.prefix, nb + 1)) return check_hip(e, "prefix");
+    launch(fill_kernel<unsigned long long>, 2, s, H.best, int64_t(2), ~0ull);
+    launch_reduce(split_min, nb + 1, s, H.prefix, nb, a, H.best);
+    launch_reduce(split_first, nb + 1, s, H.prefix, nb, a, H.best, H.best + 1);
+    launch(mark_moved, nb, s, H.corder, nb, H.best, H.best + 1, H.kept);
+    launch(fill_kernel<int64_t>, 1, s, H.kept + nb, int64_t(1), int64_t(0));
+    if (hipError_t e = x.prims.exclusive_sum(H.kept, H.kscan, nb + 1)) return check_hip(e, "kept scan");
+    launch(kept_index, nb, s, H.kept, H.kscan, nb, H.out_block);
+    launch(moved_elements, S.n + 1, s, S.elem_block, H.kept, S.n, H.eflag);
+    if (hipError_t e = x.prims.exclusive_sum(H.eflag, H.vdst, S.n + 1)) return check_hip(e, "residual scan");
+    if (spmm_status st = check_launch("hybrid split")) return st;
+    hipLaunchKernelGGL(collect_three, dim3(1), dim3(64), 0, s, H.kscan + nb, H.vdst + S.n, H.wide, S.scal);
+    if (spmm_status st = read_back(v, S.scal, 3, s)) return st;
+    if (round == 1 || v[2] == 0) break;
+  }
   *kept_out = v[0];
   *vnnz_out = v[1];
   return SPMM_OK;

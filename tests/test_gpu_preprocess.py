@@ -137,6 +137,28 @@ def test_block_level_split_bit_exact(spmm_npu, case, a):
     assert_same(got, ref)
 
 
+@pytest.mark.parametrize("window", [2, 16])
+def test_block_level_split_occupancy_beyond_the_window(spmm_npu, window):
+    """Duplicate CSR entries give a block more entries than the window has
+    rows (at least 5 at window 2, at least 42 at window 16).  The GPU split orders
+    blocks with one sort on occupancy << position bits | first element when
+    occupancies fit the window's bit width, and falls back to the two stable
+    sorts when one does not: both must equal the oracle."""
+    rng = np.random.default_rng(19)
+    crow, col = random_csr(rng, 64, 40, 6)
+    rows = [list(col[crow[r]:crow[r + 1]]) for r in range(64)]
+    rows[0] = sorted(rows[0] + [7] * (3 if window == 2 else 40))
+    rows[1] = sorted(rows[1] + [7] * 2)
+    crow = np.zeros(65, np.int64)
+    crow[1:] = np.cumsum([len(r) for r in rows])
+    col = np.concatenate([np.asarray(r, np.int64) for r in rows])
+    val = values_for(col, torch.float32)
+    ref = O.block_level_split(crow, col, val, 64, 40, 0.5, window)
+    got = spmm_npu.block_level_split(torch.from_numpy(crow), torch.from_numpy(col), torch.from_numpy(val),
+                                     64, 40, 0.5, window)
+    assert_same(got, ref)
+
+
 @pytest.mark.parametrize("window", [2, 8, 32])
 def test_block_level_split_window_sizes(spmm_npu, window):
     rng = np.random.default_rng(13)
