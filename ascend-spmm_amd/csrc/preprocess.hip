@@ -873,11 +873,17 @@ __global__ void renumber(const int64_t* __restrict__ cols, int64_t n, const int6
 }
 
 // Transpose keys: entry e goes to packed row inv[col] (stable in position order).
-__global__ void transpose_keys(const int64_t* __restrict__ col64, const int64_t* __restrict__ inv,
-                               int64_t n, uint64_t* __restrict__ key, int64_t* __restrict__ id) {
+// The transposed entry of element e goes to row inv[col] at column
+// inv[row]; the sort value carries both e and inv[row] when they fit 32 bits
+// each (packed), so transpose_entries reads no row or inverse: the elements
+// run in row order here, so these inv[row] reads are nearly sequential.
+__global__ void transpose_keys(const int64_t* __restrict__ col64, const int64_t* __restrict__ row_of,
+                               const int64_t* __restrict__ inv, int64_t n, int packed,
+                               uint64_t* __restrict__ key, int64_t* __restrict__ id) {
   GRID_STRIDE(e, n) {
     key[e] = static_cast<uint64_t>(inv[col64[e]]);
-    id[e] = e;
+    id[e] = packed ? static_cast<int64_t>((static_cast<uint64_t>(inv[row_of[e]]) << 32) | static_cast<uint64_t>(e))
+                   : e;
   }
 }
 
@@ -893,10 +899,11 @@ __global__ void transpose_rowptr(const uint64_t* __restrict__ skey, int64_t n, i
 template <typename U>
 __global__ void transpose_entries(const int64_t* __restrict__ sid, const int64_t* __restrict__ row_of,
                                   const int64_t* __restrict__ inv, const U* __restrict__ val, int64_t p_begin,
-                                  int64_t n, int64_t* __restrict__ colT, U* __restrict__ valT) {
+                                  int64_t n, int packed, int64_t* __restrict__ colT, U* __restrict__ valT) {
   GRID_STRIDE(i, n) {
-    const int64_t e = sid[i];
-    colT[i] = inv[row_of[e]];
+    const int64_t v = sid[i];
+    const int64_t e = packed ? static_cast<int64_t>(static_cast<uint64_t>(v) & 0xFFFFFFFFu) : v;
+    colT[i] = packed ? static_cast<int64_t>(static_cast<uint64_t>(v) >> 32) : inv[row_of[e]];
     valT[i] = val[p_begin + e];
   }
 }
@@ -1479,14 +1486,16 @@ spmm_status task_plan(const Csr& c, bool graph_layout, void* ws, size_t ws_bytes
     if (spmm_status st = read_back(&last, S.row_first + c.rows, 1, s)) return st;
     if (S.p_begin != 0 || S.p_begin + last != c.nnz)
       return fail(SPMM_ERR_INVALID_ARGUMENT, "CSR row pointer does not end at nnz");
-    launch(transpose_keys, n, s, S.col64, A.inv, n, A.tkey, A.tkey_id);
+    // Element ids and packed rows below 2^32 travel packed in the sort value.
+    const int packed = n <= 0xFFFFFFFFll && hs.out_rows <= 0xFFFFFFFFll ? 1 : 0;
+    launch(transpose_keys, n, s, S.col64, S.row_of, A.inv, n, packed, A.tkey, A.tkey_id);
     if (hipError_t e = x.prims.sort_pairs(A.tkey, A.stkey, A.tkey_id, A.sid, n,
                                           bits_for(static_cast<uint64_t>(hs.out_rows))))
       return check_hip(e, "transpose sort");
     launch(transpose_rowptr, n + 1, s, A.stkey, n, hs.out_rows, A.rpT);
     spmm_status st = by_value_size(c.vs(), [&](auto u) {
       using U = decltype(u);
-      launch(transpose_entries<U>, n, s, A.sid, S.row_of, A.inv, static_cast<const U*>(c.val), S.p_begin, n,
+      launch(transpose_entries<U>, n, s, A.sid, S.row_of, A.inv, static_cast<const U*>(c.val), S.p_begin, n, packed,
              A.colT, reinterpret_cast<U*>(A.valT));
       return check_launch("transpose");
     });
