@@ -72,13 +72,13 @@ OP_KERNELS = {
 FETCH_SCALE = 2.0
 WRITE_SCALE = 1.0
 PMC_KIB = {
-    (2, "csr", 128): {"fetch_kib": 222413.5, "write_kib": 32583.6, "sources": "63a90326becc6dfd",
+    (2, "csr", 128): {"fetch_kib": 222453.6, "write_kib": 32583.9, "sources": "e6fe0d6feae3382c",
                       "profile": "profiles/gather_c2_csr_n128_traffic.md"},
-    (3, "mixed", 128): {"fetch_kib": 94455.1, "write_kib": 28596.3, "sources": "63a90326becc6dfd",
+    (3, "mixed", 128): {"fetch_kib": 94400.3, "write_kib": 28596.3, "sources": "e6fe0d6feae3382c",
                         "profile": "profiles/mixed_c3_n128_traffic.md"},
-    (3, "bcsr", 128): {"fetch_kib": 38873.7, "write_kib": 16386.5, "sources": "63a90326becc6dfd",
+    (3, "bcsr", 128): {"fetch_kib": 38873.4, "write_kib": 16386.5, "sources": "e6fe0d6feae3382c",
                        "profile": "profiles/block_c3_bcsr_n128_traffic.md"},
-    (4, "mixed", 512): {"fetch_kib": 409669.6, "write_kib": 209065.4, "sources": "63a90326becc6dfd",
+    (4, "mixed", 512): {"fetch_kib": 409740.5, "write_kib": 209065.3, "sources": "e6fe0d6feae3382c",
                         "profile": "profiles/mixed_c4_n512_traffic.md"},
 }
 
