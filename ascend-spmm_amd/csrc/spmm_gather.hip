@@ -116,6 +116,20 @@ struct Geometry {
   int32_t* keys;    // [cwin]: bucket | rank within the share's bucket << kKeyRankShift
   int32_t* hist;    // [kXcds][kOrderBuckets]: windows per bucket of each share
   int32_t* nlocal;  // [kXcds]: local windows of each share
+  // Segment work-groups (seg != nullptr): a segment of a long row crossing
+  // range ends (the row's part inside one range) whose columns spread over
+  // at least an eighth of [0, K) is summed by the segment work-groups at the
+  // end of gather_tiles' grid, which deal such segments to the XCDs by
+  // column slab; seg[2j] / seg[2j + 1] describe range j's head and tail
+  // segments (written by segment_classify).
+  uint32_t* seg;
+  uint32_t* seg_flag;   // [chunks]: 1 when the chunk holds a segment (set by segment_classify)
+  int64_t seg_chunk;    // ranges per chunk of the segment work-groups (a power of two)
+  int seg_chunk_log2;
+  int range_log2;       // log2(range)
+  int64_t seg_chunks;   // chunks
+  int64_t tile_blocks;  // work-groups before the segment work-groups in gather_tiles' grid
+  float slab_scale;     // kXcds / K: column -> slab
 
   __device__ inline int64_t rp(int64_t r) const {
     return clampi(static_cast<int64_t>(rowptr[r < vrows ? r : vrows]), 0, nnz);
@@ -333,17 +347,15 @@ struct Sink {
     }
   }
 
-  // The row in progress at the range end continues into the next range:
-  // its partial goes to the head slot if it began before the range, else to
-  // the tail slot, and `crossing` (the long row crossing the range end) is
-  // returned as the range's tail row.  Returns -1 when no row is open.
-  __device__ inline int64_t finish(bool open, int64_t crossing) {
+  // The row in progress at the range end (a long row crossing it) continues
+  // into the next range: its partial goes to the head slot if it began
+  // before the range, else to the tail slot.
+  __device__ inline void finish(bool open) {
     constexpr int V = lanes::LaneVec<T>::V;
-    if (!open) return -1;
+    if (!open) return;
     float* dst = head ? head_slot : tail_slot;
 #pragma unroll
     for (int i = 0; i < V; ++i) dst[i] = acc[i];
-    return head ? -1 : crossing;
   }
 };
 
@@ -398,6 +410,133 @@ constexpr int kKeyRankShift = 10;
 static_assert(kOrderBuckets <= (1 << kKeyRankShift), "bucket ids fit below the rank");
 static_assert((kOrderMaxWindows + kXcds - 1) / kXcds < (int64_t(1) << (31 - kKeyRankShift)),
               "ranks within a share fit the key");
+
+// Segment words.  Range j has at most two segments of long rows that cross
+// range ends: the head segment [jR, min(b, (j+1)R)) of the row crossing jR,
+// and the tail segment [a, (j+1)R) of a row [a, b) starting in the range and
+// crossing (j+1)R (for a row covering the whole range, only the head).  A
+// word is kSegValid | slab << kSegSlabShift | offset, with offset the head
+// segment's end or the tail segment's start relative to jR; 0 when the
+// segment does not exist or stays with gather_tiles.  The segment's partial
+// sum is the same fp32 sequence whichever work-group computes it.
+constexpr uint32_t kSegValid = 0x80000000u;
+constexpr int kSegSlabShift = 16;
+constexpr uint32_t kSegOffsetMask = 0xFFFFu;
+static_assert(kGatherRangeMax <= static_cast<int64_t>(kSegOffsetMask), "segment offsets fit the word");
+// Chunks of the segment work-groups: the words of blockDim.x / 2 ranges (one
+// word per thread), shared by kXcds * kSegSplit work-groups (kSegSplit per
+// XCD, each taking every kSegSplit-th segment of its slab): a slab of a
+// chunk of long rows holds about blockDim.x / 16 segments, one round of lane
+// groups.
+constexpr int64_t kSegChunkRanges = kWgThreads / 2;
+#ifndef SPMM_SEG_SPLIT
+#define SPMM_SEG_SPLIT 2
+#endif
+constexpr int kSegSplit = SPMM_SEG_SPLIT;
+// Staging positions per lane and round in the segment work-groups (R / L
+// positions per lane: 8 for R = 128 at 16 lanes).
+constexpr int kSegStageUnroll = 8;
+// Batches of kBatch positions in flight per lane group in the segment
+// work-groups; segments are staged in whole groups of kSegGroup positions,
+// plus the kSegInflight - 1 batches the last group issues ahead.
+#ifndef SPMM_SEG_INFLIGHT
+#define SPMM_SEG_INFLIGHT 2
+#endif
+constexpr int kSegInflight = SPMM_SEG_INFLIGHT;
+constexpr int kSegGroup = kSegInflight * kBatch;
+// Staged positions per lane group for ranges of R positions.
+__host__ __device__ inline int64_t seg_stage_stride(int64_t range) {
+  return range + kSegGroup + (kSegInflight - 1) * kBatch;
+}
+// Segments shorter than R / kSegMinDiv positions stay with gather_tiles.
+constexpr int64_t kSegMinDiv = 8;
+// The segment work-groups run for matrices of at least kSegMinNnz nonzeros
+// (on smaller ones the extra launch costs more than the L2 hits can save)
+// whose dense operand spans at most kSegMaxDenseBytes (a column slab of 1/8
+// of it is then within twice an XCD's 4 MB L2).
+#ifndef SPMM_SEG_MIN_NNZ
+#define SPMM_SEG_MIN_NNZ (int64_t(1) << 20)
+#endif
+constexpr int64_t kSegMinNnz = SPMM_SEG_MIN_NNZ;
+constexpr int64_t kSegMaxDenseBytes = int64_t(64) << 20;
+
+// Segment words of every range, one thread per row, before gather_tiles.  A
+// long row (more than short_max(R) nonzeros) that crosses range ends is
+// split at them; its segments go to the segment work-groups when its
+// columns span at least K / kXcds (the first and last column; columns are
+// sorted within a row) and the segment holds at least R / kSegMinDiv
+// positions.  A segment's slab is the column slab (eighth of [0, K)) of its
+// middle position, its column interpolated between the row's first and last
+// columns.  Range j's head word belongs to the row holding position jR and
+// its tail word to the row holding its last position, so each call writes
+// every word of the ranges inside the rows; gather_tiles reads a word only
+// where such a row crosses the range end.  A chunk holding any segment gets
+// its flag set (cleared by the post pass).
+template <typename I>
+__global__ __launch_bounds__(kWgThreads) void segment_classify(Geometry<I> g, const I* __restrict__ col) {
+  const int64_t r = g.row_lo + static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int lane = static_cast<int>(threadIdx.x & 63);
+  const int sh = g.range_log2, csh = g.seg_chunk_log2;
+  const int64_t R = int64_t(1) << sh;
+  int64_t a = 0, b = 0, ja = 0, jb = -1;
+  bool split = false;
+  float c_first = 0.f, c_step = 0.f;
+  if (r < g.row_hi) {
+    a = g.rp(r);
+    b = g.rp(r + 1);
+    if (a < b) {
+      ja = a >> sh;
+      jb = (b - 1) >> sh;
+      if (b - a > g.short_max && ja != jb) {
+        const int64_t cf = static_cast<int64_t>(col[a]), cl = static_cast<int64_t>(col[b - 1]);
+        if (cf >= 0 && cf < g.K && cl >= 0 && cl < g.K) {
+          split = (cl > cf ? cl - cf : cf - cl) * kXcds >= g.K;
+          c_first = static_cast<float>(cf);
+          c_step = static_cast<float>(cl - cf) / static_cast<float>(b - 1 - a);
+        }
+      }
+    }
+  }
+  // Range j of row [a, b): its head word if the row holds jR, its tail
+  // word if the row holds the range's last position.
+  auto classify = [&](int64_t j, int64_t a, int64_t b, bool split, float c_first, float c_step) {
+    auto word = [&](int64_t s0, int64_t s1, int64_t offset) -> uint32_t {
+      if (!split || (s1 - s0) * kSegMinDiv < R) return 0u;
+      const float c_mid = c_first + c_step * static_cast<float>(((s0 + s1) >> 1) - a);
+      int slab = static_cast<int>(c_mid * g.slab_scale);
+      slab = slab < 0 ? 0 : (slab >= kXcds ? kXcds - 1 : slab);
+      return kSegValid | (static_cast<uint32_t>(slab) << kSegSlabShift) | static_cast<uint32_t>(offset);
+    };
+    const int64_t lo = j << sh, hi = lo + R < g.nnz ? lo + R : g.nnz;
+    if (lo >= a) {  // the row holds lo: head segment if it crosses lo
+      const int64_t e = b < hi ? b : hi;
+      const uint32_t w = a < lo ? word(lo, e, e - lo) : 0u;
+      g.seg[2 * j] = w;
+      if (w != 0u) g.seg_flag[j >> csh] = 1u;
+    }
+    if (hi <= b) {  // the row holds the range's last position: tail segment if it starts here and crosses hi
+      const uint32_t w = a >= lo && b > hi ? word(a, hi, a - lo) : 0u;
+      g.seg[2 * j + 1] = w;
+      if (w != 0u) g.seg_flag[j >> csh] = 1u;
+    }
+  };
+  // A row touching at most kClassifyOwn ranges is done by its thread; longer
+  // rows are shared by the whole wavefront, one at a time.
+  constexpr int64_t kClassifyOwn = 16;
+  const bool own = jb - ja + 1 <= kClassifyOwn;
+  if (own)
+    for (int64_t j = ja; j <= jb; ++j) classify(j, a, b, split, c_first, c_step);
+  unsigned long long shared = __ballot(!own);
+  while (shared) {
+    const int src = __ffsll(static_cast<long long>(shared)) - 1;
+    shared &= shared - 1;
+    const int64_t sa = __shfl(a, src), sb = __shfl(b, src);
+    const bool ssplit = __shfl(static_cast<int>(split), src) != 0;
+    const float sf = __shfl(c_first, src), ss = __shfl(c_step, src);
+    const int64_t sja = sa >> sh, sjb = (sb - 1) >> sh;
+    for (int64_t j = sja + lane; j <= sjb; j += 64) classify(j, sa, sb, ssplit, sf, ss);
+  }
+}
 
 // One work-group; hist: kOrderBuckets int32 of LDS.
 template <typename I>
@@ -525,11 +664,194 @@ __device__ void scatter_share(const Geometry<I>& g, int64_t part, int32_t* start
   }
 }
 
+// Segment work-groups, the last work-groups of gather_tiles' grid (wid counts
+// them from 0; wid % kXcds is the XCD they run on).  Work-group wid runs on
+// XCD x = wid % kXcds, is part h = (wid / kXcds) % kSegSplit of its XCD's
+// share, and reads the segment words of the ranges
+// [c * blockDim.x / 2, (c + 1) * blockDim.x / 2), c = wid / (kXcds * kSegSplit),
+// which segment_classify wrote before this launch.
+// It sums every kSegSplit-th segment (from h) of column slab x, so each
+// XCD's L2 serves one eighth of the dense rows these segments gather.  When
+// one slab holds more segments than its work-groups take in two rounds (a
+// row far longer than the chunk keeps its chunk inside one slab), the
+// chunk's segments are dealt in kXcds * kSegSplit equal parts of their word
+// order instead (part x * kSegSplit + h).  A lane group stages its segment's sources and
+// values in LDS (padded to whole batches with empty positions: value -0,
+// zero piece) and streams them as gather_tiles does, so the partial is the
+// same fp32 sequence, written to the range's head or tail slot.
+template <typename T, typename I>
+__device__ void segment_worker(const Geometry<I>& g, int64_t wid, const I* __restrict__ col,
+                               const T* __restrict__ value, const T* __restrict__ dense, int64_t K, int64_t N,
+                               int64_t ld, float* __restrict__ ws, int64_t slot, int log2L, int64_t chunks,
+                               unsigned char* smem) {
+  constexpr int V = LaneVec<T>::V;
+  constexpr int kWaves = kWgThreads / 64;
+  static_assert(2 * kSegChunkRanges == kWgThreads, "one segment word per thread");
+  // The work-group has gather_tiles' block size (at most kWgThreads, a
+  // multiple of 64): its chunk is blockDim.x / 2 ranges, one word per thread.
+  const int nthreads = static_cast<int>(blockDim.x);
+  const int64_t chunk_ranges = nthreads / 2;
+  const int waves = nthreads / 64;
+  __shared__ uint32_t s_word[2 * kSegChunkRanges];
+  __shared__ int32_t s_item[2 * kSegChunkRanges];
+  __shared__ int32_t s_hist[kXcds];
+  __shared__ int32_t s_wave[kWaves];
+  const int64_t range = g.range, nranges = g.nranges, nnz = g.nnz;
+  const int tid = static_cast<int>(threadIdx.x);
+  const int lane64 = tid & 63, wave = tid >> 6;
+  const int x = static_cast<int>(wid % kXcds);
+  const int h = static_cast<int>((wid / kXcds) % kSegSplit);
+  const int64_t c = wid / (kXcds * kSegSplit);
+  const int64_t w0 = c * (2 * chunk_ranges);
+  // Chunks without segments (flag clear) have nothing to do.
+  if (g.seg_flag[c] == 0u) return;  // uniform
+  const int64_t left = 2 * nranges - w0;
+  const int nw = left < 2 * chunk_ranges ? static_cast<int>(left) : nthreads;
+  const uint32_t w = tid < nw ? g.seg[w0 + tid] : 0u;
+  const bool valid = (w & kSegValid) != 0u;
+  const int slab = static_cast<int>((w >> kSegSlabShift) & (kXcds - 1));
+  s_word[tid] = w;
+  if (tid < kXcds) s_hist[tid] = 0;
+  __syncthreads();
+  if (valid) atomicAdd(&s_hist[slab], 1);
+  __syncthreads();
+  int most = 0;
+#pragma unroll
+  for (int i = 0; i < kXcds; ++i) most = s_hist[i] > most ? s_hist[i] : most;
+  const int L = 1 << log2L;
+  const int groups = nthreads >> log2L;
+  const int per_round = static_cast<int>(groups / chunks);
+  // Candidates in word order: the segments of slab x, or (parts mode) all.
+  const bool by_slab = most <= 2 * kSegSplit * per_round;
+  const bool cand = valid && (!by_slab || slab == x);
+  const unsigned long long below = (1ull << lane64) - 1ull;
+  const unsigned long long mb = __ballot(cand);
+  if (lane64 == 0) s_wave[wave] = __popcll(mb);
+  __syncthreads();
+  int m = 0, mbefore = 0;
+#pragma unroll
+  for (int i = 0; i < kWaves; ++i) {
+    mbefore += i < wave ? s_wave[i] : 0;
+    m += i < waves ? s_wave[i] : 0;
+  }
+  if (cand) s_item[mbefore + __popcll(mb & below)] = tid;
+  // This work-group's segments: candidates first, first + step, ...
+  constexpr int kParts = kXcds * kSegSplit;
+  const int q = x * kSegSplit + h;
+  const int first = by_slab ? h : static_cast<int>(int64_t(q) * m / kParts);
+  const int step = by_slab ? kSegSplit : 1;
+  const int n = by_slab ? (m > h ? (m - h + kSegSplit - 1) / kSegSplit : 0)
+                        : static_cast<int>(int64_t(q + 1) * m / kParts) - first;
+
+  __syncthreads();  // s_item complete
+
+  // Lane group g takes pairs (segment, column chunk) g, g + groups, ...; its
+  // staging area is its own and the lane group lies inside one wavefront, so
+  // staging needs only wavefront-scope ordering, and a wavefront without a
+  // pair exits at once.
+  const int group = tid >> log2L, lane = tid & (L - 1);
+  const int64_t stride = seg_stage_stride(range);
+  uint32_t* st_src = reinterpret_cast<uint32_t*>(smem) + group * stride;
+  float* st_val = reinterpret_cast<float*>(smem) + (groups + group) * stride;
+  const int64_t pairs = int64_t(n) * chunks;
+  for (int64_t p = group; p < pairs; p += groups) {
+    const int wi = s_item[first + static_cast<int>(p / chunks) * step];
+    const uint32_t word = s_word[wi];
+    const int64_t j = (w0 + wi) >> 1;
+    const int64_t lo = j * range;
+    const int64_t hi = lo + range < nnz ? lo + range : nnz;
+    const int64_t off = static_cast<int64_t>(word & kSegOffsetMask);
+    int64_t s0 = (wi & 1) ? lo + off : lo;
+    int64_t s1 = (wi & 1) ? hi : lo + off;
+    s1 = s1 < hi ? s1 : hi;
+    s0 = s0 < s1 ? s0 : s1;
+    const int64_t c0 = ((p % chunks) * L + lane) * V;
+    float* dst = ws + (2 * j + (wi & 1)) * slot + c0;
+    const int32_t n_pos = static_cast<int32_t>(s1 - s0);
+    const int32_t n_pad = (n_pos + kSegGroup - 1) / kSegGroup * kSegGroup;
+    const int32_t n_stage = n_pad + (kSegInflight - 1) * kBatch;
+    // The previous pair's staging reads are done before it is overwritten.
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    // kSegStageUnroll positions per lane per round, their loads in flight together.
+    for (int32_t i0 = 0; i0 < n_stage; i0 += kSegStageUnroll * L) {
+      I cs[kSegStageUnroll];
+      T vs[kSegStageUnroll];
+#pragma unroll
+      for (int u = 0; u < kSegStageUnroll; ++u) {
+        // Unconditional loads (clamped into the segment, n_pos >= 1 here), so
+        // no branch separates them.
+        const int32_t i = i0 + u * L + lane;
+        const int64_t q = s0 + (i < n_pos ? i : n_pos - 1);
+        cs[u] = col[q];
+        vs[u] = value[q];
+      }
+#pragma unroll
+      for (int u = 0; u < kSegStageUnroll; ++u) {
+        const int32_t i = i0 + u * L + lane;
+        if (i < n_stage) {
+          const uint32_t src =
+              i < n_pos ? BufferLoader<T>::stage(static_cast<int64_t>(cs[u]), K, ld) : BufferLoader<T>::kNone;
+          st_src[i] = src;
+          st_val[i] = src != BufferLoader<T>::kNone ? static_cast<float>(vs[u]) : -0.f;
+        }
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    if (n_pos > 0 && c0 < N) {
+      const BufferLoader<T> ldr(dense, K, ld, N, c0);
+      float acc[V];
+#pragma unroll
+      for (int i = 0; i < V; ++i) acc[i] = 0.f;
+      lanes::raw16_t xb[kSegInflight][kBatch];
+      float vb[kSegInflight][kBatch];
+      auto issue = [&](lanes::raw16_t* xs, float* vs, int32_t q) {
+#pragma unroll
+        for (int u = 0; u < kBatch; u += 4) {
+          const lanes::raw16_t s4 = *reinterpret_cast<const lanes::raw16_t*>(st_src + q + u);
+          const lanes::float4_t v4 = *reinterpret_cast<const lanes::float4_t*>(st_val + q + u);
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            xs[u + k] = ldr.load(s4[k]);
+            vs[u + k] = v4[k];
+          }
+        }
+      };
+      auto consume = [&](const lanes::raw16_t* xs, const float* vs) {
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+          float xf[V];
+          LaneVec<T>::unpack(xs[u], xf);
+#pragma unroll
+          for (int i = 0; i < V; ++i) acc[i] = __builtin_fmaf(vs[u], xf[i], acc[i]);
+        }
+      };
+      // kSegInflight batches in flight: the loads of batch k + kSegInflight - 1
+      // are issued before batch k is accumulated.  Batches past n_pad read
+      // the empty positions staged after it (no memory access) and are never
+      // accumulated.
+#pragma unroll
+      for (int b = 0; b + 1 < kSegInflight; ++b) issue(xb[b], vb[b], b * kBatch);
+      for (int32_t q = 0; q < n_pad; q += kSegGroup) {
+#pragma unroll
+        for (int b = 0; b < kSegInflight; ++b) {
+          constexpr int kAhead = kSegInflight - 1;
+          issue(xb[(b + kAhead) % kSegInflight], vb[(b + kAhead) % kSegInflight], q + (b + kAhead) * kBatch);
+          consume(xb[b], vb[b]);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < V; ++i) dst[i] = acc[i];
+    }
+  }
+}
+
 #ifndef SPMM_GATHER_WAVES
 #define SPMM_GATHER_WAVES 5
 #endif
 // Waves per SIMD the register budget of gather_tiles is fitted to.
-template <typename T, typename I, typename Loader, bool kOrder>
+// kSeg: the instantiation with segment work-groups (buffer loads, no window
+// order); the others keep the plain tile kernel's registers.
+template <typename T, typename I, typename Loader, bool kOrder, bool kSeg>
 __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM_GATHER_WAVES))) void gather_tiles(
     Geometry<I> g, const I* __restrict__ col, const T* __restrict__ value,
     const T* __restrict__ dense, int64_t K, int64_t N, int64_t ld, T* __restrict__ out, float* __restrict__ ws,
@@ -544,8 +866,10 @@ __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM
   // Per range boundary k of the tile (position P0 + k*R, k = 0..ranges):
   //  s_cut[k]:  end (relative to P0) of the short row crossing it, or -1;
   //  s_long[k]: the long row crossing it, or -1.
+  //  s_long_a[k]: that long row's first position.
   __shared__ int32_t s_cut[kTileRanges + 1];
   __shared__ int64_t s_long[kTileRanges + 1];
+  __shared__ int64_t s_long_a[kTileRanges + 1];
 
   // XCD-aware tile order: the XCD of work-group g (g % kXcds) takes column
   // part g % kXcds % wg_split of a contiguous run of tiles, so neighbouring
@@ -554,7 +878,16 @@ __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM
   // With a window order to write (kOrder: a separate instantiation, so the
   // plain gather keeps its register budget), work-groups [0, kXcds) come
   // first and write the windows' sort keys while the gathers run.
+  // With segment words (dense operands within the buffer limit only), the
+  // segment work-groups follow the tiles in the grid.
   int64_t bid = static_cast<int64_t>(blockIdx.x);
+  static_assert(!kSeg || (std::is_same<Loader, BufferLoader<T>>::value && !kOrder), "segments: buffer loads only");
+  if constexpr (kSeg) {
+    if (bid >= g.tile_blocks) {
+      segment_worker<T, I>(g, bid - g.tile_blocks, col, value, dense, K, N, ld, ws, slot, log2L, chunks, smem);
+      return;
+    }
+  }
   if constexpr (kOrder) {
     if (bid < kXcds) {
       window_keys(g, bid, reinterpret_cast<int32_t*>(smem));
@@ -634,7 +967,10 @@ __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM
         if (b - a <= g.short_max) {
           if (k <= nr && P0 + k * g.range < b) s_cut[k] = static_cast<int32_t>(b - P0);
         } else {
-          for (; k <= nr && P0 + k * g.range < b; ++k) s_long[k] = r;
+          for (; k <= nr && P0 + k * g.range < b; ++k) {
+            s_long[k] = r;
+            s_long_a[k] = a;
+          }
         }
       }
     }
@@ -657,12 +993,20 @@ __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM
   // short row this range owns past its end.  Positions from here on are
   // relative to P0.
   const int32_t cut_in = s_cut[j - j0], cut_out = s_cut[j - j0 + 1];
-  const int32_t ps = cut_in >= 0 ? cut_in : static_cast<int32_t>((lo > base ? lo : base) - P0);
-  const int32_t pe = cut_out >= 0 ? cut_out : static_cast<int32_t>((hi < end ? hi : end) - P0);
-  if (ps >= pe || c0 >= N) {
-    if (reporter) g.tail[j] = -1;
-    return;
-  }
+  int32_t ps = cut_in >= 0 ? cut_in : static_cast<int32_t>((lo > base ? lo : base) - P0);
+  int32_t pe = cut_out >= 0 ? cut_out : static_cast<int32_t>((hi < end ? hi : end) - P0);
+  // Long rows crossing the range's ends: hrow crosses lo (the range starts
+  // inside it), trow crosses hi; the tail row is trow when it starts here.
+  // Segments left to the segment work-groups are skipped here: the range
+  // then starts after the head segment and ends before the tail segment.
+  const int64_t hrow = s_long[j - j0], trow = s_long[j - j0 + 1];
+  const bool t_here = trow >= 0 && s_long_a[j - j0 + 1] >= lo;
+  const uint32_t h_word = kSeg && hrow >= 0 ? g.seg[2 * j] : 0u;
+  const uint32_t t_word = kSeg && t_here ? g.seg[2 * j + 1] : 0u;
+  if (h_word != 0u) ps = static_cast<int32_t>(lo + (h_word & kSegOffsetMask) - P0);
+  if (t_word != 0u) pe = static_cast<int32_t>(lo + (t_word & kSegOffsetMask) - P0);
+  if (reporter) g.tail[j] = t_here ? trow : -1;
+  if (ps >= pe || c0 >= N) return;
 
   Sink<T> sk;
   sk.rS = rS;
@@ -674,8 +1018,9 @@ __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM
   sk.vpart = g.vpart;
   sk.head_slot = ws + (2 * j) * slot + c0;
   sk.tail_slot = ws + (2 * j + 1) * slot + c0;
-  // The first row began before the range when a long row crosses its start.
-  sk.head = cut_in < 0 && lo > base && s_long[j - j0] >= 0;
+  // The first row began before the range when a long row crosses its start
+  // (and its head segment stays here).
+  sk.head = cut_in < 0 && lo > base && hrow >= 0 && h_word == 0u;
 #pragma unroll
   for (int i = 0; i < V; ++i) sk.acc[i] = 0.f;
 
@@ -707,8 +1052,7 @@ __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM
   } else {
     sk.consume(A);
   }
-  const int64_t tail_row = sk.finish(sa.mark[pe - 1] == 0u, s_long[j - j0 + 1]);
-  if (reporter) g.tail[j] = tail_row;
+  sk.finish(sa.mark[pe - 1] == 0u);
 }
 
 // Post pass, one launch:
@@ -718,7 +1062,8 @@ __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM
 //  * work-groups [0, fix_blocks): add the partials of every row that crosses
 //    range ends, in range order (lane group per (range, column chunk));
 //  * the next zero_blocks: zero the block kernel's window counters (mixed
-//    operator), which that kernel expects at zero;
+//    operator), which that kernel expects at zero, and clear the chunk
+//    flags of the segment work-groups for the next call;
 //  * the rest: empty rows, 64 per wavefront, are written as zeros (rows of
 //    block windows with blocks are left to the block kernel).
 template <typename T, typename I>
@@ -740,6 +1085,7 @@ __global__ __launch_bounds__(kWgThreads) void gather_post(Geometry<I> g, int64_t
   if (bid >= fix_blocks && bid < fix_blocks + zero_blocks) {
     const int64_t i = (bid - fix_blocks) * blockDim.x + threadIdx.x;
     if (i < count) zero_counts[i] = 0u;
+    if (g.seg != nullptr && i < g.seg_chunks) g.seg_flag[i] = 0u;
     return;
   }
   if (bid < fix_blocks) {
@@ -990,28 +1336,72 @@ spmm_status gather_typed(const void* rowptr, const void* col, const void* value,
   const int64_t wg_threads = groups_per_wg * L;
   const int64_t slot = gather_slot_floats(N);
 
-  // Workspace: tail rows, then the partial slots (256-byte aligned).
+  // Workspace: tail rows, the partial slots, the segment words, then the
+  // chunk flags of the segment work-groups (256-byte aligned pieces).
   const size_t tail_bytes = align_up(static_cast<size_t>(g.nranges) * sizeof(int64_t), 256);
-  const size_t need = tail_bytes + static_cast<size_t>(2 * g.nranges) * slot * sizeof(float);
+  const size_t partial_bytes = static_cast<size_t>(2 * g.nranges) * slot * sizeof(float);
+  const size_t seg_bytes = align_up(static_cast<size_t>(2 * g.nranges) * sizeof(uint32_t), 256);
+  const size_t need = tail_bytes + partial_bytes + seg_bytes + align_up(static_cast<size_t>(g.nranges) * sizeof(uint32_t), 256);
   if (ws == nullptr || ws_bytes < need)
     return fail(SPMM_ERR_CONTRACT, "gather workspace too small: need " + std::to_string(need) +
                                        " bytes, got " + std::to_string(ws_bytes));
   g.tail = static_cast<int64_t*>(ws);
   float* partial = reinterpret_cast<float*>(static_cast<char*>(ws) + tail_bytes);
 
+  // Dense operands within a 32-bit byte extent use buffer loads.
+  const int64_t extent = buffer_extent(K, ld, N, sizeof(T));
+  const bool buffer = extent <= kBufferLimit;
+  // Segment work-groups for spmm_csr on large matrices whose dense operand
+  // is at most kSegMaxDenseBytes (an XCD's column slab of it then stays near
+  // its L2).  The vector part of the mixed operator holds the rows the cost
+  // model left to the vector engine, and its calls are not worth the extra
+  // classification launch (config 3's mixed op +5 us, no wide rows).
+  // Their work-groups have gather_tiles' block size, which must hold whole
+  // wavefronts (narrow rows give smaller tiles).
+  const bool seg_on = g.cwin == 0 && g.nnz >= kSegMinNnz && K > 0 && buffer && extent <= kSegMaxDenseBytes &&
+                      wg_threads % 64 == 0;
+  g.seg = seg_on ? reinterpret_cast<uint32_t*>(static_cast<char*>(ws) + tail_bytes + partial_bytes) : nullptr;
+  g.seg_flag = seg_on ? reinterpret_cast<uint32_t*>(static_cast<char*>(ws) + tail_bytes + partial_bytes + seg_bytes)
+                      : nullptr;
+  g.seg_chunk = wg_threads / 2;
+  g.seg_chunk_log2 = 0;
+  while ((int64_t(1) << g.seg_chunk_log2) < g.seg_chunk) ++g.seg_chunk_log2;
+  g.range_log2 = 0;
+  while ((int64_t(1) << g.range_log2) < g.range) ++g.range_log2;
+  g.seg_chunks = seg_on ? ceil_div(g.nranges, g.seg_chunk) : 0;
+  g.slab_scale = K > 0 ? static_cast<float>(static_cast<double>(kXcds) / static_cast<double>(K)) : 0.f;
+  g.tile_blocks = 0;
+
   if (g.nnz > 0) {
     const int64_t tiles = ceil_div(g.nranges, ranges_per_tile);
     size_t lds = static_cast<size_t>((ranges_per_tile + 1) * g.range) * Staged<T>::bytes_per_position();
     if (g.order && lds < kOrderBuckets * sizeof(int32_t)) lds = kOrderBuckets * sizeof(int32_t);  // window_keys' histogram
-    // Dense operands within a 32-bit byte extent use buffer loads.
-    const bool buffer = buffer_extent(K, ld, N, sizeof(T)) <= kBufferLimit;
-    auto kernel = g.order ? (buffer ? gather_tiles<T, I, BufferLoader<T>, true> : gather_tiles<T, I, GlobalLoader<T>, true>)
-                          : (buffer ? gather_tiles<T, I, BufferLoader<T>, false> : gather_tiles<T, I, GlobalLoader<T>, false>);
+    auto kernel = seg_on ? gather_tiles<T, I, BufferLoader<T>, false, true>
+                  : g.order ? (buffer ? gather_tiles<T, I, BufferLoader<T>, true, false>
+                                      : gather_tiles<T, I, GlobalLoader<T>, true, false>)
+                            : (buffer ? gather_tiles<T, I, BufferLoader<T>, false, false>
+                                      : gather_tiles<T, I, GlobalLoader<T>, false, false>);
     // kXcds / wg_split groups of XCDs take runs of kXcdRun tiles in turn.
     if (kXcds % wg_split != 0) return fail(SPMM_ERR_CONTRACT, "gather: column split does not divide the XCDs");
     const int64_t groups = kXcds / wg_split;
     const int64_t tiles_per_group = ceil_div(tiles, groups * kXcdRun) * kXcdRun;
-    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(kXcds * tiles_per_group + (g.order ? kXcds : 0))),
+    g.tile_blocks = kXcds * tiles_per_group + (g.order ? kXcds : 0);
+    int64_t blocks = g.tile_blocks;
+    if (seg_on) {
+      // Segment words first, then the tiles with the segment work-groups
+      // after them in the same grid (a multiple of kXcds work-groups
+      // precedes them, so work-group b of them runs on XCD b % kXcds).
+      if ((int64_t(1) << g.seg_chunk_log2) != g.seg_chunk || (int64_t(1) << g.range_log2) != g.range)
+        return fail(SPMM_ERR_CONTRACT, "gather: segment chunks and ranges must be powers of two");
+      hipLaunchKernelGGL((segment_classify<I>), dim3(static_cast<unsigned>(ceil_div(row_hi - row_lo, kWgThreads))),
+                         dim3(kWgThreads), 0, stream, g, static_cast<const I*>(col));
+      if (spmm_status st = check_launch("segment_classify")) return st;
+      blocks += kXcds * kSegSplit * g.seg_chunks;
+      const size_t seg_lds =
+          static_cast<size_t>(wg_threads >> log2L) * seg_stage_stride(g.range) * 2 * sizeof(uint32_t);
+      if (lds < seg_lds) lds = seg_lds;
+    }
+    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks)),
                        dim3(static_cast<unsigned>(wg_threads)), lds, stream, g,
                        static_cast<const I*>(col), static_cast<const T*>(value),
                        static_cast<const T*>(dense), K, N, ld, static_cast<T*>(out), partial, log2L,
@@ -1021,7 +1411,8 @@ spmm_status gather_typed(const void* rowptr, const void* col, const void* value,
   const int64_t fix_items = g.nnz > 0 ? (g.nranges - 1) * chunks * L : 0;
   const int64_t fix_blocks = ceil_div(fix_items, kWgThreads);
   const int64_t row_blocks = ceil_div(ceil_div(row_hi - row_lo, 64), kWgThreads / 64);
-  const int64_t zero_blocks = zero_counts != nullptr ? ceil_div(count, kWgThreads) : 0;
+  const int64_t zero_items = (zero_counts != nullptr ? count : 0) > g.seg_chunks ? count : g.seg_chunks;
+  const int64_t zero_blocks = ceil_div(zero_items, kWgThreads);
   const int64_t order_blocks = g.order != nullptr ? kXcds : 0;
   const size_t post_lds = g.order != nullptr ? (kOrderBuckets + kWgThreads) * sizeof(int32_t) : 0;
   hipLaunchKernelGGL((gather_post<T, I>),
@@ -1037,7 +1428,8 @@ spmm_status gather_typed(const void* rowptr, const void* col, const void* value,
 size_t gather_workspace_bytes(int64_t nnz, int64_t width) {
   const int64_t nr = (nnz > 0 ? ceil_div(nnz, gather_range(nnz)) : 1);
   return align_up(static_cast<size_t>(nr) * sizeof(int64_t), 256) +
-         static_cast<size_t>(2 * nr) * gather_slot_floats(width) * sizeof(float);
+         static_cast<size_t>(2 * nr) * gather_slot_floats(width) * sizeof(float) +
+         align_up(static_cast<size_t>(2 * nr) * sizeof(uint32_t), 256) + align_up(static_cast<size_t>(nr) * sizeof(uint32_t), 256);
 }
 
 size_t gather_probe_sink_floats(int64_t nnz, int64_t width, int32_t value_type) {

@@ -92,6 +92,53 @@ def test_spmm_csr_long_rows_cross_ranges(spmm_npu, index_dtype):
     assert_close(out, O.spmm_f64(crow, col, vals, B), "fp32")
 
 
+def _wide_row_matrix(rng, cols):
+    """About 1.13M nonzeros (above the segment workers' 2^20 threshold): one
+    row of 110k columns (its ranges sweep a chunk inside one column slab, so
+    the workers deal that chunk in eighths), 45 rows of 20k uniform columns
+    (slab buckets) and short rows."""
+    rows = 4000
+    deg = rng.integers(0, 61, size=rows)
+    deg[10] = 110_000
+    deg[100:145] = 20_000
+    parts = [np.sort(rng.choice(cols, int(d), replace=False)) for d in deg]
+    crow = np.zeros(rows + 1, dtype=np.int64)
+    crow[1:] = np.cumsum(deg)
+    return crow, np.concatenate(parts).astype(np.int64)
+
+
+@pytest.mark.parametrize("dtype,width", [("fp16", 128), ("fp16", 256), ("fp32", 64), ("fp32", 128)])
+def test_segment_workers_equal_tile_path_bitwise(spmm_npu, dtype, width):
+    """Segments of wide long rows summed by gather_segments (dense operand of
+    at most 64 MiB) give the same bits as gather_tiles summing them (the same
+    columns in a dense operand padded past 64 MiB, which switches the workers
+    off), and both match the fp64 oracle.  fp32 uses positive operands: a
+    signed sum of 110k fp32 products cancels to values whose absolute error
+    (same bits on both paths) exceeds the 1e-4 tolerance; without
+    cancellation the tolerance holds for every element."""
+    rng = np.random.default_rng(4242 + width)
+    cols = 120_000
+    crow, col = _wide_row_matrix(rng, cols)
+    assert col.size >= 1 << 20
+    if dtype == "fp16":
+        vals = rng.uniform(-1, 1, col.size).astype(np.float16)
+        B = rng.standard_normal((cols, width)).astype(np.float16)
+    else:
+        vals = rng.uniform(0.5, 1, col.size).astype(np.float32)
+        B = (np.abs(rng.standard_normal((cols, width))) + 0.1).astype(np.float32)
+    elem = 2 if dtype == "fp16" else 4
+    assert cols * width * elem <= 64 << 20
+    pad_rows = (64 << 20) // (width * elem) + 1024
+    out = run_csr(spmm_npu, crow, col, vals, B)
+    Bpad = torch.zeros((pad_rows, width), dtype=dev(vals).dtype, device="cuda")
+    Bpad[:cols] = dev(B)
+    out_tiles = spmm_npu.spmm_csr(dev(crow, torch.int32), dev(col, torch.int32), dev(vals), Bpad,
+                                  dev(O.make_start(crow, 40)))
+    torch.cuda.synchronize()
+    assert torch.equal(out.cpu(), out_tiles.cpu())
+    assert_close(out, O.spmm_f64(crow, col, vals, B), dtype)
+
+
 def test_spmm_csr_edge_shapes(spmm_npu):
     rng = np.random.default_rng(3)
     B = rng.standard_normal((10, 16)).astype(np.float32)
