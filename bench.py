@@ -62,7 +62,9 @@ MFMA_PEAK_TFLOPS = {"fp16": 2500.0, "fp32": 157.3}
 # The kernels one timed call launches (the roofline's event time covers all
 # of them, in launch order on one stream).
 OP_KERNELS = {
-    "csr": "gather_tiles + gather_post (one spmm_csr call)",
+    "csr": ("segment_classify + gather_tiles + gather_post (one spmm_csr call; segment_classify and "
+            "gather_tiles' segment work-groups only for inputs of at least 2^20 nonzeros and a dense "
+            "operand of at most 64 MiB)"),
     "mixed-empty": "gather_tiles + gather_post (spmm_ascend_cube, empty block part)",
     "bcsr": "block_windows (+ block_zero_counts when windows can overflow)",
     "mixed": "gather_tiles + gather_post + block_windows",
@@ -72,13 +74,13 @@ OP_KERNELS = {
 FETCH_SCALE = 2.0
 WRITE_SCALE = 1.0
 PMC_KIB = {
-    (2, "csr", 128): {"fetch_kib": 222453.6, "write_kib": 32583.9, "sources": "e6fe0d6feae3382c",
+    (2, "csr", 128): {"fetch_kib": 158806.5, "write_kib": 32692.0, "sources": "63dafc0bb3b58841",
                       "profile": "profiles/gather_c2_csr_n128_traffic.md"},
-    (3, "mixed", 128): {"fetch_kib": 94400.3, "write_kib": 28596.3, "sources": "e6fe0d6feae3382c",
+    (3, "mixed", 128): {"fetch_kib": 93895.1, "write_kib": 28595.2, "sources": "63dafc0bb3b58841",
                         "profile": "profiles/mixed_c3_n128_traffic.md"},
-    (3, "bcsr", 128): {"fetch_kib": 38873.4, "write_kib": 16386.5, "sources": "e6fe0d6feae3382c",
+    (3, "bcsr", 128): {"fetch_kib": 38872.9, "write_kib": 16386.5, "sources": "63dafc0bb3b58841",
                        "profile": "profiles/block_c3_bcsr_n128_traffic.md"},
-    (4, "mixed", 512): {"fetch_kib": 409740.5, "write_kib": 209065.3, "sources": "e6fe0d6feae3382c",
+    (4, "mixed", 512): {"fetch_kib": 409766.2, "write_kib": 209053.1, "sources": "63dafc0bb3b58841",
                         "profile": "profiles/mixed_c4_n512_traffic.md"},
 }
 
