@@ -139,6 +139,55 @@ def test_segment_workers_equal_tile_path_bitwise(spmm_npu, dtype, width):
     assert_close(out, O.spmm_f64(crow, col, vals, B), dtype)
 
 
+def test_segment_workers_width_invariant_bitwise(spmm_npu):
+    """Across the segment gate: fp16 widths up to 256 use the segment
+    work-groups (K = 120k rows, at most 64 MiB), 512 and 1024 do not, and
+    C_1024[:, :n] == C_n bit for bit for every width n; int64 indices give
+    the same bits as int32."""
+    rng = np.random.default_rng(99)
+    cols = 120_000
+    crow, col = _wide_row_matrix(rng, cols)
+    vals = rng.uniform(-1, 1, col.size).astype(np.float16)
+    B = rng.standard_normal((cols, 1024)).astype(np.float16)
+    full = run_csr(spmm_npu, crow, col, vals, B).cpu()
+    for n in (16, 64, 128, 256, 512):
+        part = run_csr(spmm_npu, crow, col, vals, np.ascontiguousarray(B[:, :n])).cpu()
+        assert torch.equal(part, full[:, :n]), f"width {n} differs"
+    Bn = np.ascontiguousarray(B[:, :128])
+    assert torch.equal(run_csr(spmm_npu, crow, col, vals, Bn, torch.int64).cpu(), full[:, :128])
+    assert_close(full[:, :128], O.spmm_f64(crow, col, vals, Bn), "fp16")
+
+
+def test_segment_workers_invalid_and_unsorted_columns(spmm_npu):
+    """Wide long rows with invalid column ids (at a row's first and last
+    position and inside it) and a long row with unsorted columns: invalid
+    ids contribute nothing, and the segment path matches the fp64 oracle and
+    the tile path bit for bit."""
+    rng = np.random.default_rng(7)
+    cols = 120_000
+    crow, col = _wide_row_matrix(rng, cols)
+    r10 = slice(crow[10], crow[11])
+    col[r10] = rng.permutation(col[r10])  # unsorted columns in the 110k row
+    for r in (100, 101, 102):
+        a, b = crow[r], crow[r + 1]
+        col[a] = cols + 5          # first position invalid
+        col[b - 1] = -3 if r == 101 else cols  # last position invalid
+        col[a + (b - a) // 2] = cols + 17
+    vals = rng.uniform(-1, 1, col.size).astype(np.float16)
+    B = rng.standard_normal((cols, 128)).astype(np.float16)
+    out = spmm_npu.spmm_csr(dev(crow, torch.int32), dev(col, torch.int32), dev(vals), dev(B),
+                            dev(O.make_start(crow, 40)))
+    Bpad = torch.zeros(((64 << 20) // 256 + 1024, 128), dtype=torch.float16, device="cuda")
+    Bpad[:cols] = dev(B)
+    colp = np.where((col >= 0) & (col < cols), col, Bpad.shape[0] + 3)  # invalid for the padded operand too
+    out_tiles = spmm_npu.spmm_csr(dev(crow, torch.int32), dev(colp, torch.int32), dev(vals), Bpad,
+                                  dev(O.make_start(crow, 40)))
+    assert torch.equal(out.cpu(), out_tiles.cpu())
+    keep = (col >= 0) & (col < cols)
+    assert_close(out, O.spmm_f64(crow, np.where(keep, col, 0), np.where(keep, vals, 0).astype(np.float16), B),
+                 "fp16")
+
+
 def test_spmm_csr_edge_shapes(spmm_npu):
     rng = np.random.default_rng(3)
     B = rng.standard_normal((10, 16)).astype(np.float32)
