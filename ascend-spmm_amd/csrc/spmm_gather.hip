@@ -130,6 +130,10 @@ struct Geometry {
   int64_t seg_chunks;   // chunks
   int64_t tile_blocks;  // work-groups before the segment work-groups in gather_tiles' grid
   float slab_scale;     // kXcds / K: column -> slab
+  // [tiles]: the row holding tile t's first position t << tile_shift, which
+  // segment_classify writes in place of gather_tiles' row search.
+  int64_t* tile_row;
+  int tile_shift;
 
   __device__ inline int64_t rp(int64_t r) const {
     return clampi(static_cast<int64_t>(rowptr[r < vrows ? r : vrows]), 0, nnz);
@@ -471,7 +475,8 @@ constexpr int64_t kSegMaxDenseBytes = int64_t(64) << 20;
 // its tail word to the row holding its last position, so each call writes
 // every word of the ranges inside the rows; gather_tiles reads a word only
 // where such a row crosses the range end.  A chunk holding any segment gets
-// its flag set (cleared by the post pass).
+// its flag set (cleared by the post pass).  The row holding a tile's first
+// position is that tile's first row, recorded in tile_row.
 template <typename I>
 __global__ __launch_bounds__(kWgThreads) void segment_classify(Geometry<I> g, const I* __restrict__ col) {
   const int64_t r = g.row_lo + static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -520,21 +525,29 @@ __global__ __launch_bounds__(kWgThreads) void segment_classify(Geometry<I> g, co
       if (w != 0u) g.seg_flag[j >> csh] = 1u;
     }
   };
+  // Tiles t (first position t << tile_shift) starting in row [a, b).
+  const int ts = g.tile_shift;
+  auto tiles_of = [&](int64_t a, int64_t b, int64_t r, int first, int step) {
+    for (int64_t t = ((a + (int64_t(1) << ts) - 1) >> ts) + first; t <= ((b - 1) >> ts); t += step) g.tile_row[t] = r;
+  };
   // A row touching at most kClassifyOwn ranges is done by its thread; longer
   // rows are shared by the whole wavefront, one at a time.
   constexpr int64_t kClassifyOwn = 16;
   const bool own = jb - ja + 1 <= kClassifyOwn;
-  if (own)
+  if (own) {
     for (int64_t j = ja; j <= jb; ++j) classify(j, a, b, split, c_first, c_step);
+    if (a < b) tiles_of(a, b, r, 0, 1);
+  }
   unsigned long long shared = __ballot(!own);
   while (shared) {
     const int src = __ffsll(static_cast<long long>(shared)) - 1;
     shared &= shared - 1;
-    const int64_t sa = __shfl(a, src), sb = __shfl(b, src);
+    const int64_t sa = __shfl(a, src), sb = __shfl(b, src), sr = __shfl(r, src);
     const bool ssplit = __shfl(static_cast<int>(split), src) != 0;
     const float sf = __shfl(c_first, src), ss = __shfl(c_step, src);
     const int64_t sja = sa >> sh, sjb = (sb - 1) >> sh;
     for (int64_t j = sja + lane; j <= sjb; j += 64) classify(j, sa, sb, ssplit, sf, ss);
+    tiles_of(sa, sb, sr, lane, 64);
   }
 }
 
@@ -917,24 +930,39 @@ __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM
   }
   // rS: the row holding position P0 (tiles starting outside our positions
   // [base, end) clamp to the row range); runs of empty rows before the tile
-  // are skipped.  Every wavefront finds it by the same search.
+  // are skipped.  Every wavefront finds it by the same search, or (kSeg)
+  // reads it from tile_row, clamped to the row range (row pointers that
+  // decrease leave entries unwritten).
   int64_t rS = g.row_hi;
+  if constexpr (kSeg)
+    rS = P0 < base ? g.row_lo : (P0 < end ? clampi(g.tile_row[tile], g.row_lo, g.row_hi - 1) : g.row_hi);
+  // The tile's positions from a work-group-uniform base (P0 < nnz), 32-bit
+  // offsets clamped to the last position.
+  const I* __restrict__ col_t = col + P0;
+  const T* __restrict__ value_t = value + P0;
+  const uint32_t last = static_cast<uint32_t>(g.nnz - 1 - P0);
   for (int64_t i0 = 0; i0 < tile_positions; i0 += kStageUnroll * blockDim.x) {
     I cs[kStageUnroll];
     T vs[kStageUnroll];
+    // The block size through an empty asm: offsets recomputed per round
+    // rather than hoisted out of the loop (where they would hold kStageUnroll
+    // address registers each and spill).
+    uint32_t bd = blockDim.x;
+    __asm__ volatile("" : "+s"(bd));
 #pragma unroll
     for (int k = 0; k < kStageUnroll; ++k) {
-      if (i0 + k * blockDim.x < tile_positions) {  // uniform over the work-group
-        int64_t p = P0 + i0 + k * blockDim.x + threadIdx.x;
-        p = p < g.nnz ? p : g.nnz - 1;
-        cs[k] = col[p];
-        vs[k] = value[p];
+      if (i0 + k * bd < tile_positions) {  // uniform over the work-group
+        uint32_t o = static_cast<uint32_t>(i0 + k * bd + threadIdx.x);
+        o = o < last ? o : last;
+        cs[k] = col_t[o];
+        vs[k] = value_t[o];
       }
     }
-    if (i0 == 0) rS = P0 < base ? g.row_lo : (P0 < end ? find_row(g, P0) : g.row_hi);
+    if constexpr (!kSeg)
+      if (i0 == 0) rS = P0 < base ? g.row_lo : (P0 < end ? find_row(g, P0) : g.row_hi);
 #pragma unroll
     for (int k = 0; k < kStageUnroll; ++k) {
-      const int64_t i = i0 + k * blockDim.x + threadIdx.x;
+      const int64_t i = i0 + k * bd + threadIdx.x;
       if (i < tile_positions) {
         const uint32_t src = Loader::stage(static_cast<int64_t>(cs[k]), K, ld);
         sa.src[i] = src;
@@ -1336,12 +1364,14 @@ spmm_status gather_typed(const void* rowptr, const void* col, const void* value,
   const int64_t wg_threads = groups_per_wg * L;
   const int64_t slot = gather_slot_floats(N);
 
-  // Workspace: tail rows, the partial slots, the segment words, then the
-  // chunk flags of the segment work-groups (256-byte aligned pieces).
+  // Workspace: tail rows, the partial slots, the segment words, the chunk
+  // flags of the segment work-groups, then the tiles' first rows (256-byte
+  // aligned pieces).
   const size_t tail_bytes = align_up(static_cast<size_t>(g.nranges) * sizeof(int64_t), 256);
   const size_t partial_bytes = static_cast<size_t>(2 * g.nranges) * slot * sizeof(float);
   const size_t seg_bytes = align_up(static_cast<size_t>(2 * g.nranges) * sizeof(uint32_t), 256);
-  const size_t need = tail_bytes + partial_bytes + seg_bytes + align_up(static_cast<size_t>(g.nranges) * sizeof(uint32_t), 256);
+  const size_t flag_bytes = align_up(static_cast<size_t>(g.nranges) * sizeof(uint32_t), 256);
+  const size_t need = tail_bytes + partial_bytes + seg_bytes + flag_bytes + static_cast<size_t>(g.nranges) * sizeof(int64_t);
   if (ws == nullptr || ws_bytes < need)
     return fail(SPMM_ERR_CONTRACT, "gather workspace too small: need " + std::to_string(need) +
                                        " bytes, got " + std::to_string(ws_bytes));
@@ -1357,17 +1387,27 @@ spmm_status gather_typed(const void* rowptr, const void* col, const void* value,
   // model left to the vector engine, and its calls are not worth the extra
   // classification launch (config 3's mixed op +5 us, no wide rows).
   // Their work-groups have gather_tiles' block size, which must hold whole
-  // wavefronts (narrow rows give smaller tiles).
+  // wavefronts (narrow rows give smaller tiles); chunks, ranges and tiles
+  // span powers of two (segment_classify works with shifts).
+  auto log2_of = [](int64_t v) {
+    int l = 0;
+    while ((int64_t(1) << l) < v) ++l;
+    return l;
+  };
+  g.seg_chunk = wg_threads / 2;
+  g.seg_chunk_log2 = log2_of(g.seg_chunk);
+  g.range_log2 = log2_of(g.range);
+  g.tile_shift = log2_of(ranges_per_tile * g.range);
+  const bool pow2 = (int64_t(1) << g.seg_chunk_log2) == g.seg_chunk && (int64_t(1) << g.range_log2) == g.range &&
+                    (int64_t(1) << g.tile_shift) == ranges_per_tile * g.range;
   const bool seg_on = g.cwin == 0 && g.nnz >= kSegMinNnz && K > 0 && buffer && extent <= kSegMaxDenseBytes &&
-                      wg_threads % 64 == 0;
+                      wg_threads % 64 == 0 && pow2;
   g.seg = seg_on ? reinterpret_cast<uint32_t*>(static_cast<char*>(ws) + tail_bytes + partial_bytes) : nullptr;
   g.seg_flag = seg_on ? reinterpret_cast<uint32_t*>(static_cast<char*>(ws) + tail_bytes + partial_bytes + seg_bytes)
                       : nullptr;
-  g.seg_chunk = wg_threads / 2;
-  g.seg_chunk_log2 = 0;
-  while ((int64_t(1) << g.seg_chunk_log2) < g.seg_chunk) ++g.seg_chunk_log2;
-  g.range_log2 = 0;
-  while ((int64_t(1) << g.range_log2) < g.range) ++g.range_log2;
+  g.tile_row = seg_on ? reinterpret_cast<int64_t*>(static_cast<char*>(ws) + tail_bytes + partial_bytes + seg_bytes +
+                                                    flag_bytes)
+                      : nullptr;
   g.seg_chunks = seg_on ? ceil_div(g.nranges, g.seg_chunk) : 0;
   g.slab_scale = K > 0 ? static_cast<float>(static_cast<double>(kXcds) / static_cast<double>(K)) : 0.f;
   g.tile_blocks = 0;
@@ -1388,11 +1428,10 @@ spmm_status gather_typed(const void* rowptr, const void* col, const void* value,
     g.tile_blocks = kXcds * tiles_per_group + (g.order ? kXcds : 0);
     int64_t blocks = g.tile_blocks;
     if (seg_on) {
-      // Segment words first, then the tiles with the segment work-groups
-      // after them in the same grid (a multiple of kXcds work-groups
-      // precedes them, so work-group b of them runs on XCD b % kXcds).
-      if ((int64_t(1) << g.seg_chunk_log2) != g.seg_chunk || (int64_t(1) << g.range_log2) != g.range)
-        return fail(SPMM_ERR_CONTRACT, "gather: segment chunks and ranges must be powers of two");
+      // Segment words and tile rows first, then the tiles with the segment
+      // work-groups after them in the same grid (a multiple of kXcds
+      // work-groups precedes them, so work-group b of them runs on XCD
+      // b % kXcds).
       hipLaunchKernelGGL((segment_classify<I>), dim3(static_cast<unsigned>(ceil_div(row_hi - row_lo, kWgThreads))),
                          dim3(kWgThreads), 0, stream, g, static_cast<const I*>(col));
       if (spmm_status st = check_launch("segment_classify")) return st;
@@ -1429,7 +1468,8 @@ size_t gather_workspace_bytes(int64_t nnz, int64_t width) {
   const int64_t nr = (nnz > 0 ? ceil_div(nnz, gather_range(nnz)) : 1);
   return align_up(static_cast<size_t>(nr) * sizeof(int64_t), 256) +
          static_cast<size_t>(2 * nr) * gather_slot_floats(width) * sizeof(float) +
-         align_up(static_cast<size_t>(2 * nr) * sizeof(uint32_t), 256) + align_up(static_cast<size_t>(nr) * sizeof(uint32_t), 256);
+         align_up(static_cast<size_t>(2 * nr) * sizeof(uint32_t), 256) + align_up(static_cast<size_t>(nr) * sizeof(uint32_t), 256) +
+         static_cast<size_t>(nr) * sizeof(int64_t);
 }
 
 size_t gather_probe_sink_floats(int64_t nnz, int64_t width, int32_t value_type) {
