@@ -523,7 +523,13 @@ __global__ __launch_bounds__(64 * kMaxWaves) __attribute__((amdgpu_waves_per_eu(
     const int64_t idx = g / kXcds;
     int64_t s = ((idx / kBlockXcdRun) * kXcds + g % kXcds) * kBlockXcdRun + idx % kBlockXcdRun;
     if (s >= a.windows) return;  // uniform over the work-group
-    if (a.order != nullptr) s = a.order[s];
+    if (a.order != nullptr) {
+      // The order is written earlier in the same call; an entry outside
+      // [0, windows) (a workspace shared by overlapping calls) is skipped
+      // rather than used as an index.
+      s = a.order[s];
+      if (s < 0 || s >= a.windows) return;  // uniform over the work-group
+    }
     const int64_t b0 = a.crp(s);
     int64_t b1 = a.crp(s + 1);
     if (b1 <= b0) {  // empty window: its rows are the vector pass's, or zeros

@@ -1033,6 +1033,9 @@ __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM
   const uint32_t t_word = kSeg && t_here ? g.seg[2 * j + 1] : 0u;
   if (h_word != 0u) ps = static_cast<int32_t>(lo + (h_word & kSegOffsetMask) - P0);
   if (t_word != 0u) pe = static_cast<int32_t>(lo + (t_word & kSegOffsetMask) - P0);
+  // A word's offset lies inside its range; one that does not (a workspace
+  // another call overwrote) must still not run past the staged positions.
+  if (kSeg && pe > tile_positions) pe = static_cast<int32_t>(tile_positions);
   if (reporter) g.tail[j] = t_here ? trow : -1;
   if (ps >= pe || c0 >= N) return;
 

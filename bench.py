@@ -74,13 +74,13 @@ OP_KERNELS = {
 FETCH_SCALE = 2.0
 WRITE_SCALE = 1.0
 PMC_KIB = {
-    (2, "csr", 128): {"fetch_kib": 158036.2, "write_kib": 32708.3, "sources": "242524c30e07a8dd",
+    (2, "csr", 128): {"fetch_kib": 157975.4, "write_kib": 32708.3, "sources": "266ac225ad2dc1d2",
                       "profile": "profiles/gather_c2_csr_n128_traffic.md"},
-    (3, "mixed", 128): {"fetch_kib": 93811.7, "write_kib": 28595.5, "sources": "242524c30e07a8dd",
+    (3, "mixed", 128): {"fetch_kib": 93893.1, "write_kib": 28595.3, "sources": "266ac225ad2dc1d2",
                         "profile": "profiles/mixed_c3_n128_traffic.md"},
-    (3, "bcsr", 128): {"fetch_kib": 38875.2, "write_kib": 16386.5, "sources": "242524c30e07a8dd",
+    (3, "bcsr", 128): {"fetch_kib": 38866.2, "write_kib": 16386.5, "sources": "266ac225ad2dc1d2",
                        "profile": "profiles/block_c3_bcsr_n128_traffic.md"},
-    (4, "mixed", 512): {"fetch_kib": 409621.2, "write_kib": 209051.9, "sources": "242524c30e07a8dd",
+    (4, "mixed", 512): {"fetch_kib": 409576.7, "write_kib": 209050.9, "sources": "266ac225ad2dc1d2",
                         "profile": "profiles/mixed_c4_n512_traffic.md"},
 }
 
