@@ -265,14 +265,16 @@ struct GlobalLoader {
   }
 };
 
-// One batch of kBatch consecutive positions: the lanes' 16-byte dense
-// pieces, values and row-end marks.  Positions outside [ps, pe) carry source
-// kNone (zero piece), value -0 and mark 0.
-template <typename T>
+// One batch of B consecutive positions (B a multiple of 4): the lanes'
+// 16-byte dense pieces, values and row-end marks.  Positions outside
+// [ps, pe) carry source kNone (zero piece), value -0 and mark 0.
+template <typename T, int B = kBatch>
 struct Batch {
-  lanes::raw16_t x[kBatch];
-  float v[kBatch];
-  uint32_t m[kBatch];
+  static_assert(B % 4 == 0 && (B & (B - 1)) == 0, "batches are read 4 positions at a time");
+  static constexpr int kSize = B;
+  lanes::raw16_t x[B];
+  float v[B];
+  uint32_t m[B];
 };
 
 // Issues the dense loads of a batch from the staged arrays.  Positions are
@@ -286,10 +288,10 @@ struct Stream {
   Loader ld;
   int32_t ps, pe;
 
-  template <bool kMasked>
-  __device__ inline void issue(Batch<T>& b, int32_t p0) const {
+  template <bool kMasked, int B>
+  __device__ inline void issue(Batch<T, B>& b, int32_t p0) const {
 #pragma unroll
-    for (int q = 0; q < kBatch; q += 4) {
+    for (int q = 0; q < B; q += 4) {
       // A masked batch reads no aligned group past the one holding pe - 1.
       const int32_t pq = !kMasked || p0 + q < pe ? p0 + q : ((pe - 1) & ~3);
       const lanes::raw16_t c4 = *reinterpret_cast<const lanes::raw16_t*>(s.src + pq);
@@ -339,10 +341,11 @@ struct Sink {
     for (int i = 0; i < V; ++i) acc[i] = 0.f;
   }
 
-  __device__ inline void consume(const Batch<T>& b) {
+  template <int B>
+  __device__ inline void consume(const Batch<T, B>& b) {
     constexpr int V = lanes::LaneVec<T>::V;
 #pragma unroll
-    for (int u = 0; u < kBatch; ++u) {
+    for (int u = 0; u < B; ++u) {
       float x[V];
       lanes::LaneVec<T>::unpack(b.x[u], x);
 #pragma unroll
@@ -440,17 +443,28 @@ constexpr int kSegSplit = SPMM_SEG_SPLIT;
 // Staging positions per lane and round in the segment work-groups (R / L
 // positions per lane: 8 for R = 128 at 16 lanes).
 constexpr int kSegStageUnroll = 8;
-// Batches of kBatch positions in flight per lane group in the segment
+// The segment path's gather_tiles instantiation (its tiles and its segment
+// work-groups) reads kSegBatch dense rows per batch, at kSegWaves waves per
+// SIMD (twice the rows in flight of the other instantiations, whose 4-row
+// batches fit 5 waves; 8-row batches there would spill).
+#ifndef SPMM_SEG_BATCH
+#define SPMM_SEG_BATCH 8
+#endif
+#ifndef SPMM_SEG_WAVES
+#define SPMM_SEG_WAVES 4
+#endif
+constexpr int kSegBatch = SPMM_SEG_BATCH;
+// Batches of kSegBatch positions in flight per lane group in the segment
 // work-groups; segments are staged in whole groups of kSegGroup positions,
 // plus the kSegInflight - 1 batches the last group issues ahead.
 #ifndef SPMM_SEG_INFLIGHT
 #define SPMM_SEG_INFLIGHT 2
 #endif
 constexpr int kSegInflight = SPMM_SEG_INFLIGHT;
-constexpr int kSegGroup = kSegInflight * kBatch;
+constexpr int kSegGroup = kSegInflight * kSegBatch;
 // Staged positions per lane group for ranges of R positions.
 __host__ __device__ inline int64_t seg_stage_stride(int64_t range) {
-  return range + kSegGroup + (kSegInflight - 1) * kBatch;
+  return range + kSegGroup + (kSegInflight - 1) * kSegBatch;
 }
 // Segments shorter than R / kSegMinDiv positions stay with gather_tiles.
 constexpr int64_t kSegMinDiv = 8;
@@ -782,7 +796,7 @@ __device__ void segment_worker(const Geometry<I>& g, int64_t wid, const I* __res
     float* dst = ws + (2 * j + (wi & 1)) * slot + c0;
     const int32_t n_pos = static_cast<int32_t>(s1 - s0);
     const int32_t n_pad = (n_pos + kSegGroup - 1) / kSegGroup * kSegGroup;
-    const int32_t n_stage = n_pad + (kSegInflight - 1) * kBatch;
+    const int32_t n_stage = n_pad + (kSegInflight - 1) * kSegBatch;
     // The previous pair's staging reads are done before it is overwritten.
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     // kSegStageUnroll positions per lane per round, their loads in flight together.
@@ -815,11 +829,11 @@ __device__ void segment_worker(const Geometry<I>& g, int64_t wid, const I* __res
       float acc[V];
 #pragma unroll
       for (int i = 0; i < V; ++i) acc[i] = 0.f;
-      lanes::raw16_t xb[kSegInflight][kBatch];
-      float vb[kSegInflight][kBatch];
+      lanes::raw16_t xb[kSegInflight][kSegBatch];
+      float vb[kSegInflight][kSegBatch];
       auto issue = [&](lanes::raw16_t* xs, float* vs, int32_t q) {
 #pragma unroll
-        for (int u = 0; u < kBatch; u += 4) {
+        for (int u = 0; u < kSegBatch; u += 4) {
           const lanes::raw16_t s4 = *reinterpret_cast<const lanes::raw16_t*>(st_src + q + u);
           const lanes::float4_t v4 = *reinterpret_cast<const lanes::float4_t*>(st_val + q + u);
 #pragma unroll
@@ -831,7 +845,7 @@ __device__ void segment_worker(const Geometry<I>& g, int64_t wid, const I* __res
       };
       auto consume = [&](const lanes::raw16_t* xs, const float* vs) {
 #pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
+        for (int u = 0; u < kSegBatch; ++u) {
           float xf[V];
           LaneVec<T>::unpack(xs[u], xf);
 #pragma unroll
@@ -843,12 +857,12 @@ __device__ void segment_worker(const Geometry<I>& g, int64_t wid, const I* __res
       // the empty positions staged after it (no memory access) and are never
       // accumulated.
 #pragma unroll
-      for (int b = 0; b + 1 < kSegInflight; ++b) issue(xb[b], vb[b], b * kBatch);
+      for (int b = 0; b + 1 < kSegInflight; ++b) issue(xb[b], vb[b], b * kSegBatch);
       for (int32_t q = 0; q < n_pad; q += kSegGroup) {
 #pragma unroll
         for (int b = 0; b < kSegInflight; ++b) {
           constexpr int kAhead = kSegInflight - 1;
-          issue(xb[(b + kAhead) % kSegInflight], vb[(b + kAhead) % kSegInflight], q + (b + kAhead) * kBatch);
+          issue(xb[(b + kAhead) % kSegInflight], vb[(b + kAhead) % kSegInflight], q + (b + kAhead) * kSegBatch);
           consume(xb[b], vb[b]);
         }
       }
@@ -861,11 +875,11 @@ __device__ void segment_worker(const Geometry<I>& g, int64_t wid, const I* __res
 #ifndef SPMM_GATHER_WAVES
 #define SPMM_GATHER_WAVES 5
 #endif
-// Waves per SIMD the register budget of gather_tiles is fitted to.
-// kSeg: the instantiation with segment work-groups (buffer loads, no window
-// order); the others keep the plain tile kernel's registers.
+// Waves per SIMD the register budget of gather_tiles is fitted to:
+// SPMM_GATHER_WAVES, or SPMM_SEG_WAVES for the instantiation with segment
+// work-groups (buffer loads, no window order, kSegBatch-row batches).
 template <typename T, typename I, typename Loader, bool kOrder, bool kSeg>
-__global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM_GATHER_WAVES))) void gather_tiles(
+__global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(kSeg ? SPMM_SEG_WAVES : SPMM_GATHER_WAVES))) void gather_tiles(
     Geometry<I> g, const I* __restrict__ col, const T* __restrict__ value,
     const T* __restrict__ dense, int64_t K, int64_t N, int64_t ld, T* __restrict__ out, float* __restrict__ ws,
     int log2L, int64_t chunks, int64_t ranges_per_tile, int64_t slot, int wg_split, int64_t tiles,
@@ -1055,26 +1069,27 @@ __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(SPMM
 #pragma unroll
   for (int i = 0; i < V; ++i) sk.acc[i] = 0.f;
 
-  // Two batches of kBatch dense rows in flight: the loads of the next batch
-  // are issued before a batch is accumulated.  The first batch (4-aligned
+  // Two batches of kB dense rows in flight: the loads of the next batch
+  // are issued before a batch is accumulated.  The first batch (kB-aligned
   // start, positions before ps masked) and the last two are issued masked;
   // the steady-state loop only issues batches wholly inside [ps, pe).
+  constexpr int kB = kSeg ? kSegBatch : kBatch;
   const Stream<T, Loader> st{sa, Loader(dense, K, ld, N, c0), ps, pe};
-  int32_t p = ps & ~(kBatch - 1);
-  Batch<T> A, B;
+  int32_t p = ps & ~(kB - 1);
+  Batch<T, kB> A, B;
   st.template issue<true>(A, p);
-  for (; p + 3 * kBatch <= pe; p += 2 * kBatch) {
-    st.template issue<false>(B, p + kBatch);
+  for (; p + 3 * kB <= pe; p += 2 * kB) {
+    st.template issue<false>(B, p + kB);
     sk.consume(A);
-    st.template issue<false>(A, p + 2 * kBatch);
+    st.template issue<false>(A, p + 2 * kB);
     sk.consume(B);
   }
   // A holds batch p; at most two more batches start before pe.
-  if (p + kBatch < pe) {
-    st.template issue<true>(B, p + kBatch);
+  if (p + kB < pe) {
+    st.template issue<true>(B, p + kB);
     sk.consume(A);
-    if (p + 2 * kBatch < pe) {
-      st.template issue<true>(A, p + 2 * kBatch);
+    if (p + 2 * kB < pe) {
+      st.template issue<true>(A, p + 2 * kB);
       sk.consume(B);
       sk.consume(A);
     } else {
