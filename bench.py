@@ -74,13 +74,13 @@ OP_KERNELS = {
 FETCH_SCALE = 2.0
 WRITE_SCALE = 1.0
 PMC_KIB = {
-    (2, "csr", 128): {"fetch_kib": 157975.4, "write_kib": 32708.3, "sources": "266ac225ad2dc1d2",
+    (2, "csr", 128): {"fetch_kib": 151925.5, "write_kib": 32708.3, "sources": "aa112c188196e493",
                       "profile": "profiles/gather_c2_csr_n128_traffic.md"},
-    (3, "mixed", 128): {"fetch_kib": 93893.1, "write_kib": 28595.3, "sources": "266ac225ad2dc1d2",
+    (3, "mixed", 128): {"fetch_kib": 93887.4, "write_kib": 28595.4, "sources": "aa112c188196e493",
                         "profile": "profiles/mixed_c3_n128_traffic.md"},
-    (3, "bcsr", 128): {"fetch_kib": 38866.2, "write_kib": 16386.5, "sources": "266ac225ad2dc1d2",
+    (3, "bcsr", 128): {"fetch_kib": 38867.8, "write_kib": 16386.5, "sources": "aa112c188196e493",
                        "profile": "profiles/block_c3_bcsr_n128_traffic.md"},
-    (4, "mixed", 512): {"fetch_kib": 409576.7, "write_kib": 209050.9, "sources": "266ac225ad2dc1d2",
+    (4, "mixed", 512): {"fetch_kib": 409571.2, "write_kib": 209050.2, "sources": "aa112c188196e493",
                         "profile": "profiles/mixed_c4_n512_traffic.md"},
 }
 
