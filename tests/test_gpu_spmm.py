@@ -188,6 +188,64 @@ def test_segment_workers_invalid_and_unsorted_columns(spmm_npu):
                  "fp16")
 
 
+def _boundary_matrix(rng, cols, target_nnz=1_700_000):
+    """Rows whose ends fall on range and tile starts (multiples of 128 and
+    of 2048 positions: the ranges and 16-range tiles of gather_tiles at
+    R = 128, which the library picks for 1.57M-3.1M nonzeros), runs of empty
+    rows right at tile starts, long rows (over R/2 nonzeros) crossing one or
+    several tiles, and short rows; columns spread over [0, cols), so the
+    long rows' segments go to the segment work-groups."""
+    R, span = 128, 2048
+    degs, pos = [], 0
+    while pos < target_nnz:
+        kind = int(rng.integers(0, 6))
+        if kind == 0:  # run on to the next tile start, then empty rows
+            new = [span - pos % span] + [0] * int(rng.integers(1, 4))
+        elif kind == 1:  # run on to the next range start
+            new = [R - pos % R]
+        elif kind == 2:  # a long row over several tiles
+            new = [int(rng.integers(3 * span, 5 * span))]
+        elif kind == 3:  # a long row of one or a few ranges
+            new = [int(rng.integers(R // 2 + 1, 1000))]
+        else:
+            new = [int(x) for x in rng.integers(1, 40, size=8)]
+        degs += new
+        pos += sum(new)
+    deg = np.array(degs, dtype=np.int64)
+    crow = np.zeros(deg.size + 1, dtype=np.int64)
+    crow[1:] = np.cumsum(deg)
+    col = np.concatenate([np.sort(rng.choice(cols, int(d), replace=False)) for d in deg if d > 0])
+    return crow, col.astype(np.int64)
+
+
+def test_segment_path_row_boundaries_on_tile_starts(spmm_npu):
+    """The segment path's classification records each tile's first row for
+    gather_tiles: tiles starting exactly at a row's first position, after a
+    run of empty rows, or inside a long row crossing several tiles all read
+    the right row.  Compared bit for bit with the tile path (the same columns
+    in a dense operand padded past 64 MiB) and with the fp64 oracle."""
+    rng = np.random.default_rng(2048)
+    cols = 120_000
+    crow, col = _boundary_matrix(rng, cols)
+    nnz = col.size
+    assert 1_572_864 <= nnz < 3_145_728  # R = 128: 2 R 12288 <= nnz < 4 R 12288
+    ends = crow[1:]
+    deg = np.diff(crow)
+    empty_at_tile = (deg == 0) & (crow[:-1] % 2048 == 0)
+    assert int((ends % 2048 == 0).sum()) > 50 and int(empty_at_tile.sum()) > 50
+    assert int(((crow[:-1] // 2048) + 2 <= (ends - 1) // 2048).sum()) > 20  # rows crossing 2+ tile starts
+    vals = rng.uniform(-1, 1, nnz).astype(np.float16)
+    B = rng.standard_normal((cols, 128)).astype(np.float16)
+    out = run_csr(spmm_npu, crow, col, vals, B)
+    Bpad = torch.zeros(((64 << 20) // 256 + 1024, 128), dtype=torch.float16, device="cuda")
+    Bpad[:cols] = dev(B)
+    out_tiles = spmm_npu.spmm_csr(dev(crow, torch.int32), dev(col, torch.int32), dev(vals), Bpad,
+                                  dev(O.make_start(crow, 40)))
+    assert torch.equal(out.cpu(), out_tiles.cpu())
+    assert_close(out, O.spmm_f64(crow, col, vals, B), "fp16")
+    assert bool((out[torch.from_numpy(deg == 0).cuda()] == 0).all())
+
+
 def test_spmm_csr_edge_shapes(spmm_npu):
     rng = np.random.default_rng(3)
     B = rng.standard_normal((10, 16)).astype(np.float32)
