@@ -129,6 +129,7 @@ struct Geometry {
   int range_log2;       // log2(range)
   int64_t seg_chunks;   // chunks
   int64_t tile_blocks;  // work-groups before the segment work-groups in gather_tiles' grid
+  int seg_split;        // segment work-groups per XCD and chunk (seg_split_for)
   float slab_scale;     // kXcds / K: column -> slab
   // [tiles]: the row holding tile t's first position t << tile_shift, which
   // segment_classify writes in place of gather_tiles' row search.
@@ -452,15 +453,14 @@ constexpr int kSegSlabShift = 16;
 constexpr uint32_t kSegOffsetMask = 0xFFFFu;
 static_assert(kGatherRangeMax <= static_cast<int64_t>(kSegOffsetMask), "segment offsets fit the word");
 // Chunks of the segment work-groups: the words of blockDim.x / 2 ranges (one
-// word per thread), shared by kXcds * kSegSplit work-groups (kSegSplit per
-// XCD, each taking every kSegSplit-th segment of its slab): a slab of a
+// word per thread), shared by kXcds * seg_split work-groups (seg_split per
+// XCD, each taking every seg_split-th segment of its slab): a slab of a
 // chunk of long rows holds about blockDim.x / 16 segments, one round of lane
-// groups.
+// groups.  seg_split grows with the lanes a segment needs (its column
+// chunks times L): 1 up to 8 lanes, 2 for one chunk of 16, 3 for two
+// chunks (each best of 1-4 on config 2 at fp16 N = 64, 128 and 256).
 constexpr int64_t kSegChunkRanges = kWgThreads / 2;
-#ifndef SPMM_SEG_SPLIT
-#define SPMM_SEG_SPLIT 2
-#endif
-constexpr int kSegSplit = SPMM_SEG_SPLIT;
+inline int seg_split_for(int64_t chunks, int L) { return chunks * L <= 8 ? 1 : (chunks == 1 ? 2 : 3); }
 // Staging positions per lane and round in the segment work-groups (R / L
 // positions per lane: 8 for R = 128 at 16 lanes).
 constexpr int kSegStageUnroll = 8;
@@ -714,16 +714,16 @@ __device__ void scatter_share(const Geometry<I>& g, int64_t part, int32_t* start
 
 // Segment work-groups, the last work-groups of gather_tiles' grid (wid counts
 // them from 0; wid % kXcds is the XCD they run on).  Work-group wid runs on
-// XCD x = wid % kXcds, is part h = (wid / kXcds) % kSegSplit of its XCD's
+// XCD x = wid % kXcds, is part h = (wid / kXcds) % seg_split of its XCD's
 // share, and reads the segment words of the ranges
-// [c * blockDim.x / 2, (c + 1) * blockDim.x / 2), c = wid / (kXcds * kSegSplit),
+// [c * blockDim.x / 2, (c + 1) * blockDim.x / 2), c = wid / (kXcds * seg_split),
 // which segment_classify wrote before this launch.
-// It sums every kSegSplit-th segment (from h) of column slab x, so each
+// It sums every seg_split-th segment (from h) of column slab x, so each
 // XCD's L2 serves one eighth of the dense rows these segments gather.  When
 // one slab holds more segments than its work-groups take in two rounds (a
 // row far longer than the chunk keeps its chunk inside one slab), the
-// chunk's segments are dealt in kXcds * kSegSplit equal parts of their word
-// order instead (part x * kSegSplit + h).  A lane group stages its segment's sources and
+// chunk's segments are dealt in kXcds * seg_split equal parts of their word
+// order instead (part x * seg_split + h).  A lane group stages its segment's sources and
 // values in LDS (padded to whole batches with empty positions: value -0,
 // zero piece) and streams them as gather_tiles does, so the partial is the
 // same fp32 sequence, written to the range's head or tail slot.
@@ -748,8 +748,9 @@ __device__ void segment_worker(const Geometry<I>& g, int64_t wid, const I* __res
   const int tid = static_cast<int>(threadIdx.x);
   const int lane64 = tid & 63, wave = tid >> 6;
   const int x = static_cast<int>(wid % kXcds);
-  const int h = static_cast<int>((wid / kXcds) % kSegSplit);
-  const int64_t c = wid / (kXcds * kSegSplit);
+  const int split = g.seg_split;
+  const int h = static_cast<int>((wid / kXcds) % split);
+  const int64_t c = wid / (kXcds * split);
   const int64_t w0 = c * (2 * chunk_ranges);
   // Chunks without segments (flag clear) have nothing to do.
   if (g.seg_flag[c] == 0u) return;  // uniform
@@ -770,7 +771,7 @@ __device__ void segment_worker(const Geometry<I>& g, int64_t wid, const I* __res
   const int groups = nthreads >> log2L;
   const int per_round = static_cast<int>(groups / chunks);
   // Candidates in word order: the segments of slab x, or (parts mode) all.
-  const bool by_slab = most <= 2 * kSegSplit * per_round;
+  const bool by_slab = most <= 2 * split * per_round;
   const bool cand = valid && (!by_slab || slab == x);
   const unsigned long long below = (1ull << lane64) - 1ull;
   const unsigned long long mb = __ballot(cand);
@@ -784,12 +785,12 @@ __device__ void segment_worker(const Geometry<I>& g, int64_t wid, const I* __res
   }
   if (cand) s_item[mbefore + __popcll(mb & below)] = tid;
   // This work-group's segments: candidates first, first + step, ...
-  constexpr int kParts = kXcds * kSegSplit;
-  const int q = x * kSegSplit + h;
-  const int first = by_slab ? h : static_cast<int>(int64_t(q) * m / kParts);
-  const int step = by_slab ? kSegSplit : 1;
-  const int n = by_slab ? (m > h ? (m - h + kSegSplit - 1) / kSegSplit : 0)
-                        : static_cast<int>(int64_t(q + 1) * m / kParts) - first;
+  const int parts = kXcds * split;
+  const int q = x * split + h;
+  const int first = by_slab ? h : static_cast<int>(int64_t(q) * m / parts);
+  const int step = by_slab ? split : 1;
+  const int n = by_slab ? (m > h ? (m - h + split - 1) / split : 0)
+                        : static_cast<int>(int64_t(q + 1) * m / parts) - first;
 
   __syncthreads();  // s_item complete
 
@@ -1448,6 +1449,7 @@ spmm_status gather_typed(const void* rowptr, const void* col, const void* value,
                                                     flag_bytes)
                       : nullptr;
   g.seg_chunks = seg_on ? ceil_div(g.nranges, g.seg_chunk) : 0;
+  g.seg_split = seg_split_for(chunks, L);
   g.slab_scale = K > 0 ? static_cast<float>(static_cast<double>(kXcds) / static_cast<double>(K)) : 0.f;
   g.tile_blocks = 0;
 
@@ -1474,7 +1476,7 @@ spmm_status gather_typed(const void* rowptr, const void* col, const void* value,
       hipLaunchKernelGGL((segment_classify<I>), dim3(static_cast<unsigned>(ceil_div(row_hi - row_lo, kWgThreads))),
                          dim3(kWgThreads), 0, stream, g, static_cast<const I*>(col));
       if (spmm_status st = check_launch("segment_classify")) return st;
-      blocks += kXcds * kSegSplit * g.seg_chunks;
+      blocks += kXcds * g.seg_split * g.seg_chunks;
       const size_t seg_lds =
           static_cast<size_t>(wg_threads >> log2L) * seg_stage_stride(g.range) * 2 * sizeof(uint32_t);
       if (lds < seg_lds) lds = seg_lds;
