@@ -492,12 +492,13 @@ constexpr int64_t kSegMinDiv = 8;
 // The segment work-groups run for matrices of at least kSegMinNnz nonzeros
 // (on smaller ones the extra launch costs more than the L2 hits can save)
 // whose dense operand spans at most kSegMaxDenseBytes (a column slab of 1/8
-// of it is then within twice an XCD's 4 MB L2).
+// of it is then within four times an XCD's 4 MB L2; config 2 at N = 512,
+// 102 MB, gains 2%, while at 205 MB config 2 at N = 1024 loses 3%).
 #ifndef SPMM_SEG_MIN_NNZ
 #define SPMM_SEG_MIN_NNZ (int64_t(1) << 20)
 #endif
 constexpr int64_t kSegMinNnz = SPMM_SEG_MIN_NNZ;
-constexpr int64_t kSegMaxDenseBytes = int64_t(64) << 20;
+constexpr int64_t kSegMaxDenseBytes = int64_t(128) << 20;
 
 // Segment words of every range, one thread per row, before gather_tiles.  A
 // long row (more than short_max(R) nonzeros) that crosses range ends is

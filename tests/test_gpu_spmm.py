@@ -15,6 +15,10 @@ import torch
 import oracle as O
 import workloads as W
 
+# The segment path's dense-operand limit (kSegMaxDenseBytes): a larger dense
+# operand takes the tile path.
+SEG_MAX_DENSE = 128 << 20
+
 pytestmark = pytest.mark.gpu
 
 TOL = {"fp16": 2e-2, "fp32": 1e-4}
@@ -110,8 +114,8 @@ def _wide_row_matrix(rng, cols):
 @pytest.mark.parametrize("dtype,width", [("fp16", 128), ("fp16", 256), ("fp32", 64), ("fp32", 128)])
 def test_segment_workers_equal_tile_path_bitwise(spmm_npu, dtype, width):
     """Segments of wide long rows summed by gather_segments (dense operand of
-    at most 64 MiB) give the same bits as gather_tiles summing them (the same
-    columns in a dense operand padded past 64 MiB, which switches the workers
+    at most 128 MiB) give the same bits as gather_tiles summing them (the same
+    columns in a dense operand padded past 128 MiB, which switches the workers
     off), and both match the fp64 oracle.  fp32 uses positive operands: a
     signed sum of 110k fp32 products cancels to values whose absolute error
     (same bits on both paths) exceeds the 1e-4 tolerance; without
@@ -127,8 +131,8 @@ def test_segment_workers_equal_tile_path_bitwise(spmm_npu, dtype, width):
         vals = rng.uniform(0.5, 1, col.size).astype(np.float32)
         B = (np.abs(rng.standard_normal((cols, width))) + 0.1).astype(np.float32)
     elem = 2 if dtype == "fp16" else 4
-    assert cols * width * elem <= 64 << 20
-    pad_rows = (64 << 20) // (width * elem) + 1024
+    assert cols * width * elem <= SEG_MAX_DENSE
+    pad_rows = SEG_MAX_DENSE // (width * elem) + 1024
     out = run_csr(spmm_npu, crow, col, vals, B)
     Bpad = torch.zeros((pad_rows, width), dtype=dev(vals).dtype, device="cuda")
     Bpad[:cols] = dev(B)
@@ -140,8 +144,8 @@ def test_segment_workers_equal_tile_path_bitwise(spmm_npu, dtype, width):
 
 
 def test_segment_workers_width_invariant_bitwise(spmm_npu):
-    """Across the segment gate: fp16 widths up to 256 use the segment
-    work-groups (K = 120k rows, at most 64 MiB), 512 and 1024 do not, and
+    """Across the segment gate: fp16 widths up to 512 use the segment
+    work-groups (K = 120k rows, at most 128 MiB), 1024 does not, and
     C_1024[:, :n] == C_n bit for bit for every width n; int64 indices give
     the same bits as int32."""
     rng = np.random.default_rng(99)
@@ -177,7 +181,7 @@ def test_segment_workers_invalid_and_unsorted_columns(spmm_npu):
     B = rng.standard_normal((cols, 128)).astype(np.float16)
     out = spmm_npu.spmm_csr(dev(crow, torch.int32), dev(col, torch.int32), dev(vals), dev(B),
                             dev(O.make_start(crow, 40)))
-    Bpad = torch.zeros(((64 << 20) // 256 + 1024, 128), dtype=torch.float16, device="cuda")
+    Bpad = torch.zeros((SEG_MAX_DENSE // 256 + 1024, 128), dtype=torch.float16, device="cuda")
     Bpad[:cols] = dev(B)
     colp = np.where((col >= 0) & (col < cols), col, Bpad.shape[0] + 3)  # invalid for the padded operand too
     out_tiles = spmm_npu.spmm_csr(dev(crow, torch.int32), dev(colp, torch.int32), dev(vals), Bpad,
@@ -223,7 +227,7 @@ def test_segment_path_row_boundaries_on_tile_starts(spmm_npu):
     gather_tiles: tiles starting exactly at a row's first position, after a
     run of empty rows, or inside a long row crossing several tiles all read
     the right row.  Compared bit for bit with the tile path (the same columns
-    in a dense operand padded past 64 MiB) and with the fp64 oracle."""
+    in a dense operand padded past 128 MiB) and with the fp64 oracle."""
     rng = np.random.default_rng(2048)
     cols = 120_000
     crow, col = _boundary_matrix(rng, cols)
@@ -237,7 +241,7 @@ def test_segment_path_row_boundaries_on_tile_starts(spmm_npu):
     vals = rng.uniform(-1, 1, nnz).astype(np.float16)
     B = rng.standard_normal((cols, 128)).astype(np.float16)
     out = run_csr(spmm_npu, crow, col, vals, B)
-    Bpad = torch.zeros(((64 << 20) // 256 + 1024, 128), dtype=torch.float16, device="cuda")
+    Bpad = torch.zeros((SEG_MAX_DENSE // 256 + 1024, 128), dtype=torch.float16, device="cuda")
     Bpad[:cols] = dev(B)
     out_tiles = spmm_npu.spmm_csr(dev(crow, torch.int32), dev(col, torch.int32), dev(vals), Bpad,
                                   dev(O.make_start(crow, 40)))
