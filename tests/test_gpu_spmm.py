@@ -250,6 +250,39 @@ def test_segment_path_row_boundaries_on_tile_starts(spmm_npu):
     assert bool((out[torch.from_numpy(deg == 0).cuda()] == 0).all())
 
 
+@pytest.mark.parametrize("seed,dtype,width", [(1, "fp16", 64), (2, "fp16", 128), (3, "fp16", 256),
+                                              (4, "fp32", 32), (5, "fp32", 64), (6, "fp32", 128)])
+def test_segment_path_random_power_law_bitwise(spmm_npu, seed, dtype, width):
+    """Seeded power-law matrices above the segment threshold (degrees from a
+    Pareto tail up to 40k, some empty rows), at widths that take each
+    segment split (1, 2 and 3 work-groups per slab): the segment path equals
+    the tile path bit for bit and the fp64 oracle within tolerance.  fp32
+    uses positive operands (long signed fp32 sums cancel past 1e-4)."""
+    rng = np.random.default_rng(5000 + seed)
+    cols, rows = 60_000, 30_000
+    deg = np.minimum((rng.pareto(1.3, rows) * 12).astype(np.int64), 40_000)
+    deg[rng.random(rows) < 0.05] = 0
+    deg = (deg * (1_300_000 / max(int(deg.sum()), 1))).astype(np.int64).clip(0, 40_000)
+    crow = np.zeros(rows + 1, dtype=np.int64)
+    crow[1:] = np.cumsum(deg)
+    col = np.concatenate([np.sort(rng.choice(cols, int(d), replace=False)) for d in deg if d > 0]).astype(np.int64)
+    assert col.size >= 1 << 20 and int(deg.max()) > 4096
+    if dtype == "fp16":
+        vals = rng.uniform(-1, 1, col.size).astype(np.float16)
+        B = rng.standard_normal((cols, width)).astype(np.float16)
+    else:
+        vals = rng.uniform(0.5, 1, col.size).astype(np.float32)
+        B = (np.abs(rng.standard_normal((cols, width))) + 0.1).astype(np.float32)
+    elem = 2 if dtype == "fp16" else 4
+    out = run_csr(spmm_npu, crow, col, vals, B)
+    Bpad = torch.zeros((SEG_MAX_DENSE // (width * elem) + 1024, width), dtype=dev(vals).dtype, device="cuda")
+    Bpad[:cols] = dev(B)
+    out_tiles = spmm_npu.spmm_csr(dev(crow, torch.int32), dev(col, torch.int32), dev(vals), Bpad,
+                                  dev(O.make_start(crow, 40)))
+    assert torch.equal(out.cpu(), out_tiles.cpu())
+    assert_close(out, O.spmm_f64(crow, col, vals, B), dtype)
+
+
 def test_spmm_csr_edge_shapes(spmm_npu):
     rng = np.random.default_rng(3)
     B = rng.standard_normal((10, 16)).astype(np.float32)
