@@ -272,7 +272,6 @@ struct GlobalLoader {
 template <typename T, int B = kBatch>
 struct Batch {
   static_assert(B % 4 == 0 && (B & (B - 1)) == 0, "batches are read 4 positions at a time");
-  static constexpr int kSize = B;
   lanes::raw16_t x[B];
   float v[B];
   uint32_t m[B];
@@ -465,8 +464,8 @@ inline int seg_split_for(int64_t chunks, int L) { return chunks * L <= 8 ? 1 : (
 // positions per lane: 8 for R = 128 at 16 lanes).
 constexpr int kSegStageUnroll = 8;
 // The segment path's gather_tiles instantiation (its tiles and its segment
-// work-groups) reads kSegBatch dense rows per batch, at kSegWaves waves per
-// SIMD (twice the rows in flight of the other instantiations, whose 4-row
+// work-groups) reads kSegBatch dense rows per batch, at SPMM_SEG_WAVES waves
+// per SIMD (twice the rows in flight of the other instantiations, whose 4-row
 // batches fit 5 waves; 8-row batches there would spill).
 #ifndef SPMM_SEG_BATCH
 #define SPMM_SEG_BATCH 8
