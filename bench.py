@@ -74,13 +74,13 @@ OP_KERNELS = {
 FETCH_SCALE = 2.0
 WRITE_SCALE = 1.0
 PMC_KIB = {
-    (2, "csr", 128): {"fetch_kib": 151525.6, "write_kib": 32708.4, "sources": "a125e9a06841c1b9",
+    (2, "csr", 128): {"fetch_kib": 151438.6, "write_kib": 32708.4, "sources": "5350da94a0c95ceb",
                       "profile": "profiles/gather_c2_csr_n128_traffic.md"},
-    (3, "mixed", 128): {"fetch_kib": 93975.3, "write_kib": 28595.4, "sources": "a125e9a06841c1b9",
+    (3, "mixed", 128): {"fetch_kib": 93813.5, "write_kib": 28595.4, "sources": "5350da94a0c95ceb",
                         "profile": "profiles/mixed_c3_n128_traffic.md"},
-    (3, "bcsr", 128): {"fetch_kib": 38867.7, "write_kib": 16386.5, "sources": "a125e9a06841c1b9",
+    (3, "bcsr", 128): {"fetch_kib": 38867.1, "write_kib": 16386.5, "sources": "5350da94a0c95ceb",
                        "profile": "profiles/block_c3_bcsr_n128_traffic.md"},
-    (4, "mixed", 512): {"fetch_kib": 409585.5, "write_kib": 209050.2, "sources": "a125e9a06841c1b9",
+    (4, "mixed", 512): {"fetch_kib": 409567.7, "write_kib": 209051.3, "sources": "5350da94a0c95ceb",
                         "profile": "profiles/mixed_c4_n512_traffic.md"},
 }
 
