@@ -54,16 +54,18 @@ def test_spmm_csr_graph_replays(spmm_npu, dtype):
     assert out.shape == (w.rows, 128)
 
 
-def test_spmm_csr_graph_replays_segment_path(spmm_npu):
-    """Config 2 at full size (2.0M nonzeros, a 25.6 MB dense operand): the
-    segment path's three launches (classification, tiles with segment
-    work-groups, post pass) replay from the graph like the eager call."""
+@pytest.mark.parametrize("width", [64, 128, 256])
+def test_spmm_csr_graph_replays_segment_path(spmm_npu, width):
+    """Config 2 at full size (2.0M nonzeros, dense operands of 12.8-51.2 MB):
+    the segment path's three launches (classification, tiles with segment
+    work-groups, post pass) replay from the graph like the eager call, at
+    widths taking 1, 2 and 3 segment work-groups per slab."""
     w = W.config2()
     assert w.nnz >= 1 << 20
-    B = dev(w.dense(128))
+    B = dev(w.dense(width))
     args = (dev(w.crow, torch.int32), dev(w.col, torch.int32), dev(w.values), B, dev(O.make_start(w.crow, 40)))
     out = check_replays(spmm_npu.spmm_csr, args, B)
-    assert out.shape == (w.rows, 128)
+    assert out.shape == (w.rows, width)
 
 
 @pytest.mark.parametrize("graph_layout", [False, True])
