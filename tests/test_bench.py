@@ -27,8 +27,9 @@ def test_bench_rejects_more_than_one_gpu():
 def test_algorithmic_bytes_closed_form():
     """bytes = 4(M+1) + (4 + s)nnz + s N K_ref + s M N, K_ref = distinct
     columns: a hand-counted 3x5 CSR, and configuration 1 against the
-    survey's figure of 17,891,332 bytes (which counts all 16384 columns;
-    the generated matrix leaves a few unused)."""
+    closed form with every column counted, 4*16385 + 8*131072 + 2*4*16384*128
+    = 17,891,332 bytes at fp32 N=128 (the generated matrix leaves a few
+    columns unused)."""
     import numpy as np
 
     import workloads as W
