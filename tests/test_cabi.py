@@ -41,6 +41,12 @@ class MixedDesc(ctypes.Structure):
 def lib():
     if not os.path.exists(LIB):
         pytest.fail(f"{LIB} is not built (python ascend-spmm_amd/build.py)")
+    # torch first, also when this file runs alone: the library's
+    # libamdhip64.so.7 dependency then resolves (by SONAME) to the HIP runtime
+    # torch loaded.  Loaded the other way round, torch brings a second
+    # runtime into the process, and the one initialised second finds no device.
+    import torch  # noqa: F401
+
     lib = ctypes.CDLL(LIB)
     lib.spmm_last_error.restype = ctypes.c_char_p
     lib.spmm_version.restype = ctypes.c_char_p
@@ -308,3 +314,56 @@ def test_rowscalar_baseline_matches_oracle_and_csr(lib, value_type, N):
     assert np.allclose(out.float().cpu().numpy(), expected, atol=tol, rtol=tol)
     short = deg <= 8
     assert torch.equal(out.cpu()[torch.from_numpy(short)], ref.cpu()[torch.from_numpy(short)])
+
+
+@pytest.mark.gpu
+def test_segment_path_ignores_workspace_contents(lib):
+    """spmm_csr on the segment path (config 2 at full size, 2.0M nonzeros, N=128
+    fp16) keeps its segment words, chunk flags and tile first rows in the
+    workspace.  The result must not depend on what the workspace held: a
+    workspace of 0xFF bytes (every chunk flag set, every tile row -1), and
+    the same workspace after a call on the row-reversed matrix (whose long
+    rows, segments and tile rows sit elsewhere), give the bits of a call on a
+    zeroed workspace, over outputs pre-filled with NaN."""
+    import torch
+
+    import workloads as W
+
+    w = W.config2()
+    N = 128
+    crow = w.crow.astype(np.int64)
+    deg = np.diff(crow)
+    # The row-reversed matrix: row r of it is row rows-1-r of config 2.
+    new_row = (w.rows - 1) - np.repeat(np.arange(w.rows), deg)
+    perm = np.argsort(new_row, kind="stable")
+    crow2 = np.concatenate([[0], np.cumsum(deg[::-1])])
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    p = lambda x: ctypes.c_void_p(x.data_ptr())
+    first = [t(crow.astype(np.int32)), t(w.col.astype(np.int32)), t(w.values)]
+    second = [t(crow2.astype(np.int32)), t(w.col[perm].astype(np.int32)), t(w.values[perm])]
+    B = t(w.dense(N))
+    d = CsrDesc(w.rows, w.nnz, w.cols, N, 0, 0)
+    assert w.nnz >= 1 << 20 and B.dtype == torch.float16
+    ws_bytes = ctypes.c_size_t(0)
+    assert lib.spmm_csr_workspace(ctypes.byref(d), ctypes.byref(ws_bytes)) == 0
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def run(mat, ws):
+        out = torch.full((w.rows, N), float("nan"), dtype=torch.float16, device="cuda")
+        rc = lib.spmm_csr_run(ctypes.byref(d), *[p(x) for x in mat], p(B), p(out), p(ws),
+                              ctypes.c_size_t(ws_bytes.value), stream)
+        assert rc == 0, lib.spmm_last_error()
+        return out
+
+    expected = run(first, torch.zeros(ws_bytes.value, dtype=torch.uint8, device="cuda"))
+    ws = torch.full((ws_bytes.value,), 255, dtype=torch.uint8, device="cuda")
+    got_ff = run(first, ws)
+    other = run(second, ws)
+    got_reused = run(first, ws)
+    torch.cuda.synchronize()
+    assert not torch.isnan(expected).any()
+    assert torch.equal(got_ff, expected)
+    assert torch.equal(got_reused, expected)
+    # the reversed matrix's rows are config 2's rows, reversed, summed in the
+    # same ranges only where the row boundaries line up: compare with tolerance
+    assert torch.allclose(other.flip(0).float(), expected.float(), atol=2e-2, rtol=2e-2)
