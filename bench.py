@@ -64,7 +64,7 @@ MFMA_PEAK_TFLOPS = {"fp16": 2500.0, "fp32": 157.3}
 OP_KERNELS = {
     "csr": ("segment_classify + gather_tiles + gather_post (one spmm_csr call; segment_classify and "
             "gather_tiles' segment work-groups only for inputs of at least 2^20 nonzeros and a dense "
-            "operand of at most 64 MiB)"),
+            "operand of at most 128 MiB)"),
     "mixed-empty": "gather_tiles + gather_post (spmm_ascend_cube, empty block part)",
     "bcsr": "block_windows (+ block_zero_counts when windows can overflow)",
     "mixed": "gather_tiles + gather_post + block_windows",
@@ -82,6 +82,14 @@ PMC_KIB = {
                        "profile": "profiles/block_c3_bcsr_n128_traffic.md"},
     (4, "mixed", 512): {"fetch_kib": 409567.7, "write_kib": 209051.3, "sources": "5350da94a0c95ceb",
                         "profile": "profiles/mixed_c4_n512_traffic.md"},
+    (1, "csr", 128): {"fetch_kib": 15809.6, "write_kib": 8256.0, "sources": "5350da94a0c95ceb",
+                      "profile": "profiles/gather_c1_csr_n128_traffic.md"},
+    (3, "csr", 128): {"fetch_kib": 98284.5, "write_kib": 73071.9, "sources": "5350da94a0c95ceb",
+                      "profile": "profiles/gather_c3_csr_n128_traffic.md"},
+    (3, "mixed", 256): {"fetch_kib": 171483.0, "write_kib": 56968.0, "sources": "5350da94a0c95ceb",
+                        "profile": "profiles/mixed_c3_n256_traffic.md"},
+    (4, "mixed", 64): {"fetch_kib": 56263.1, "write_kib": 26255.1, "sources": "5350da94a0c95ceb",
+                       "profile": "profiles/mixed_c4_n64_traffic.md"},
 }
 
 

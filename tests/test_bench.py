@@ -106,3 +106,23 @@ def test_traffic_table_is_keyed_to_the_kernel_sources():
     finally:
         del bench.PMC_KIB[key]
     assert bench.measured_traffic(98, "csr", 16)[0] is None
+
+
+def test_traffic_table_matches_its_profiles():
+    """Every entry of the PMC table names a committed profile that records
+    the same kernel-sources hash and whose per-kernel FETCH_SIZE and
+    WRITE_SIZE columns sum to the entry's figures (spmm:: kernels of the op,
+    the probe excluded)."""
+    import re
+
+    sys.path.insert(0, REPO)
+    import bench
+
+    for key, e in bench.PMC_KIB.items():
+        text = open(os.path.join(REPO, e["profile"])).read()
+        assert f"Kernel sources of the run: {e['sources']}" in text, key
+        fetch = write = 0.0
+        for row in re.findall(r"^\| `spmm::[^`]*` \| \d+ \| ([\d.]+) \| ([\d.]+) \|", text, flags=re.M):
+            fetch += float(row[0])
+            write += float(row[1])
+        assert abs(fetch - e["fetch_kib"]) < 0.5 and abs(write - e["write_kib"]) < 0.5, key
