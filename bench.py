@@ -1,6 +1,6 @@
 """Benchmark of the MI355X SpMM hot path (one JSON line on stdout).
 
-Default workload: benchmark configuration 2 (power-law CSR 100000x100000, ~1.9M nnz,
+Default workload: benchmark configuration 2 (power-law CSR 100000x100000, ~2.0M nnz,
 N=128 fp16, fp32 accumulate) — the configuration the headline metric
 "SpMM GFLOP/s (2*nnz*N/t) and HBM GB/s % of peak, N=128 fp16" is quoted on.
 A step is one SpMM call over resident device inputs.
@@ -74,21 +74,21 @@ OP_KERNELS = {
 FETCH_SCALE = 2.0
 WRITE_SCALE = 1.0
 PMC_KIB = {
-    (2, "csr", 128): {"fetch_kib": 151438.6, "write_kib": 32708.4, "sources": "5350da94a0c95ceb",
+    (2, "csr", 128): {"fetch_kib": 151572.3, "write_kib": 32708.4, "sources": "cbf5889d1f4d90d6",
                       "profile": "profiles/gather_c2_csr_n128_traffic.md"},
-    (3, "mixed", 128): {"fetch_kib": 93813.5, "write_kib": 28595.4, "sources": "5350da94a0c95ceb",
+    (3, "mixed", 128): {"fetch_kib": 93497.2, "write_kib": 28595.4, "sources": "cbf5889d1f4d90d6",
                         "profile": "profiles/mixed_c3_n128_traffic.md"},
-    (3, "bcsr", 128): {"fetch_kib": 38867.1, "write_kib": 16386.5, "sources": "5350da94a0c95ceb",
+    (3, "bcsr", 128): {"fetch_kib": 38896.7, "write_kib": 16386.5, "sources": "cbf5889d1f4d90d6",
                        "profile": "profiles/block_c3_bcsr_n128_traffic.md"},
-    (4, "mixed", 512): {"fetch_kib": 409567.7, "write_kib": 209051.3, "sources": "5350da94a0c95ceb",
+    (4, "mixed", 512): {"fetch_kib": 409510.4, "write_kib": 209050.2, "sources": "cbf5889d1f4d90d6",
                         "profile": "profiles/mixed_c4_n512_traffic.md"},
-    (1, "csr", 128): {"fetch_kib": 15809.6, "write_kib": 8256.0, "sources": "5350da94a0c95ceb",
+    (1, "csr", 128): {"fetch_kib": 15809.8, "write_kib": 8256.0, "sources": "cbf5889d1f4d90d6",
                       "profile": "profiles/gather_c1_csr_n128_traffic.md"},
-    (3, "csr", 128): {"fetch_kib": 98284.5, "write_kib": 73071.9, "sources": "5350da94a0c95ceb",
+    (3, "csr", 128): {"fetch_kib": 98276.6, "write_kib": 73071.9, "sources": "cbf5889d1f4d90d6",
                       "profile": "profiles/gather_c3_csr_n128_traffic.md"},
-    (3, "mixed", 256): {"fetch_kib": 171483.0, "write_kib": 56968.0, "sources": "5350da94a0c95ceb",
+    (3, "mixed", 256): {"fetch_kib": 171098.0, "write_kib": 56967.8, "sources": "cbf5889d1f4d90d6",
                         "profile": "profiles/mixed_c3_n256_traffic.md"},
-    (4, "mixed", 64): {"fetch_kib": 56263.1, "write_kib": 26255.1, "sources": "5350da94a0c95ceb",
+    (4, "mixed", 64): {"fetch_kib": 56263.4, "write_kib": 26255.1, "sources": "cbf5889d1f4d90d6",
                        "profile": "profiles/mixed_c4_n64_traffic.md"},
 }
 
