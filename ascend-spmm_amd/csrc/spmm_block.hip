@@ -117,13 +117,20 @@ constexpr int64_t k_step() { return sizeof(T) == 2 ? 32 : 16; }
 // of a dense row) or 8 (a 16-byte fp16 piece).  Sixteen lanes cover a column
 // group of 16 * C columns, and a K-step runs C MFMAs, one per column of the
 // piece.  fp16 takes C = 8 for outputs of at least 256 columns (two or more
-// waves per window); narrower outputs keep C = 4, so a window still has two
-// waves at N = 128.  The MFMA sequence of an output element does not depend
-// on C.
+// waves per window), and at 128 columns when there are at least
+// kWideMinWindows windows: one wave then sums a window's 128 columns, and
+// half the waves of C = 4 let every window of a large grid be resident at
+// once (config 3, N=128: 35 -> 25 us).  Fewer windows keep C = 4 at 128
+// columns, whose two waves per window fill more of the chip (config 2's
+// preprocess layout, 687 windows: 110 us with C = 4, 132 us with C = 8).
+// The MFMA sequence of an output element does not depend on C.
 template <int C>
 using half_c = _Float16 __attribute__((ext_vector_type(C)));
+constexpr int64_t kWideMinWindows = 2048;
 template <typename T>
-constexpr int lane_cols_for(int64_t N) { return sizeof(T) == 2 && N >= 256 ? 8 : 4; }
+constexpr int lane_cols_for(int64_t N, int64_t windows) {
+  return sizeof(T) == 2 && (N >= 256 || (N >= 128 && windows >= kWideMinWindows)) ? 8 : 4;
+}
 
 // The piece of a dense row one lane loads per block.
 template <typename T, int C>
@@ -207,21 +214,39 @@ __device__ inline int64_t row_stride(const BlockArgs<T, I>& a) {
   return kS ? a.ld : a.N;
 }
 
+// LDS staging of one chunk of blocks [b0, b1) (b1 - b0 <= stage): the
+// loader's source per block column, checked against K here once.  Loads are
+// issued kStageUnroll per thread before any LDS write, so a chunk costs one
+// round trip per kStageUnroll * blockDim.x blocks.  The chunk is padded to a
+// whole K-step with invalid sources, so the MFMA loop reads LDS without
+// bounds checks.  The blocks' values are not staged: each wave streams them
+// one K-step at a time (group_sum).  With `finish` set it also returns the
+// window's vector-row bits (bit r: row 16*s + r has vector-part nonzeros,
+// whose fp32 sum is in vpart), read in the same round trip.
+constexpr int kStageUnroll = 2;
+
 template <typename T, typename I, typename Loader, bool kS>
 __device__ inline unsigned stage_chunk(const BlockArgs<T, I>& a, int64_t s, bool finish, int64_t b0,
-                                       int64_t b1, uint32_t* s_src, T* s_val) {
+                                       int64_t b1, uint32_t* s_src) {
   __shared__ unsigned s_vec;
   const int64_t n = b1 - b0;
   const int64_t n_pad = (n + k_step<T>() - 1) / k_step<T>() * k_step<T>();
   if (threadIdx.x == 0) s_vec = 0;
   const bool vec = finish && threadIdx.x < 16 && a.row_has_vector(16 * s + threadIdx.x);
-  for (int64_t i = threadIdx.x; i < n_pad; i += blockDim.x)
-    s_src[i] = i < n ? Loader::stage(static_cast<int64_t>(a.Ccol[b0 + i]), a.K, row_stride<kS>(a)) : Loader::kNone;
-  constexpr int64_t kPer = 16 * sizeof(T) / 16;  // 16-byte pieces per block
-  const lanes::raw16_t* src = reinterpret_cast<const lanes::raw16_t*>(a.Cvalue + 16 * b0);
-  lanes::raw16_t* dst = reinterpret_cast<lanes::raw16_t*>(s_val);
-  for (int64_t i = threadIdx.x; i < n_pad * kPer; i += blockDim.x)
-    dst[i] = i < n * kPer ? src[i] : lanes::raw16_t{0u, 0u, 0u, 0u};
+  const int64_t nt = blockDim.x;
+  for (int64_t i0 = 0; i0 < n_pad; i0 += kStageUnroll * nt) {
+    I c[kStageUnroll];
+#pragma unroll
+    for (int u = 0; u < kStageUnroll; ++u) {
+      const int64_t i = i0 + u * nt + threadIdx.x;
+      c[u] = i < n ? a.Ccol[b0 + i] : static_cast<I>(-1);
+    }
+#pragma unroll
+    for (int u = 0; u < kStageUnroll; ++u) {
+      const int64_t i = i0 + u * nt + threadIdx.x;
+      if (i < n_pad) s_src[i] = i < n ? Loader::stage(static_cast<int64_t>(c[u]), a.K, row_stride<kS>(a)) : Loader::kNone;
+    }
+  }
   __syncthreads();
   if (vec) atomicOr(&s_vec, 1u << threadIdx.x);
   __syncthreads();
@@ -240,67 +265,94 @@ __device__ inline void store_cols(T* p, const float* v) {
   }
 }
 
-// One K-step of one lane: its dense pieces (kPieces blocks) and A values.
+// One K-step of one lane: its dense pieces (kPieces blocks) and its 16-byte
+// piece of the step's block values (a K-step's values are 1 KB for either
+// type: 32 fp16 blocks or 16 fp32 blocks of 16 rows; lane l holds bytes
+// [16 l, 16 l + 16)).
 template <typename T, int C>
 struct StepOperands {
   static constexpr int kPieces = sizeof(T) == 2 ? 8 : 4;
   Piece<T, C> x[kPieces];
-  typename std::conditional<sizeof(T) == 2, half8_t, float4_t>::type av;
+  lanes::raw16_t v;
 };
+
+// Bytes of a wave's ring for the A fragments in LDS: two K-steps of 1 KB.
+constexpr size_t kRingBytes = 2 * 1024;
 
 // MFMA sum of staged blocks [0, n) for the column group at n0.  Lane
 // (q = lane % 16, kg = lane / 16) loads columns n0 + C*q .. n0 + C*q + C-1
 // of its blocks' dense rows with one load per block (16 lanes read
 // 16 * C * sizeof(T) contiguous bytes); MFMA j takes element j of each load,
 // so its B column q is the dense column n0 + C*q + j and the accumulator lane
-// holds C consecutive output columns of rows 4kg .. 4kg+3.  With C = 4 the
-// loads of the next K-step are issued before the current step's MFMAs (two
-// steps of operands in registers).  Adds to `acc`.
+// holds C consecutive output columns of rows 4kg .. 4kg+3.  The A fragment
+// comes from the blocks' values, `vals` (the chunk's first block), which the
+// wave streams one K-step at a time: each lane loads one 16-byte piece of
+// the step's 1 KB of values with the step's dense pieces, and at multiply
+// time the wave writes the step to its LDS ring and reads the fragment
+// A[r][k] = value[16 k + r] back (LDS operations of one wave complete in
+// order; the wavefront fence keeps the compiler from moving the reads above
+// the write).  The loads of the next K-step are issued before the current
+// step's MFMAs (two steps of operands in registers).  Adds to `acc`.
 template <typename T, typename I, int C, typename Loader, bool kS>
-__device__ inline void group_sum(const BlockArgs<T, I>& a, const uint32_t* s_src, const T* s_val,
-                                 int64_t n, int64_t n0, int lane, float4_t (&acc)[C]) {
+__device__ inline void group_sum(const BlockArgs<T, I>& a, const uint32_t* s_src, const T* vals,
+                                 unsigned char* ring, int64_t n, int64_t n0, int lane, float4_t (&acc)[C]) {
   static_assert(C == 4 || (C == 8 && sizeof(T) == 2), "lane columns: 4, or 8 for fp16");
   const int q = lane & 15, kg = lane >> 4;
   const int64_t col0 = n0 + C * q < a.N ? n0 + C * q : 0;  // N % C == 0
   const Loader ld(a.dense, a.K, row_stride<kS>(a), a.N, col0);
   if (a.K <= 0 || n <= 0) return;  // uniform: no valid dense row
   const int32_t steps = static_cast<int32_t>((n + k_step<T>() - 1) / k_step<T>());
+  // 16-byte pieces of the chunk's values; pieces past them (the padding of
+  // the last K-step) are zeros.
+  const lanes::raw16_t* vpieces = reinterpret_cast<const lanes::raw16_t*>(vals);
+  const int64_t vlimit = n * static_cast<int64_t>(sizeof(T));  // 16 values per block: 16 * n * sizeof(T) / 16 pieces
 
   // fp16: the lane's 8 blocks of a 32-block step are consecutive (8kg ..);
   // fp32: its 4 blocks of a 16-block step are kg, kg+4, kg+8, kg+12.
   auto fetch = [&](StepOperands<T, C>& o, int32_t st) {
+    const int64_t piece = static_cast<int64_t>(st) * 64 + lane;
+    o.v = piece < vlimit ? vpieces[piece] : lanes::raw16_t{0u, 0u, 0u, 0u};
 #pragma unroll
     for (int e = 0; e < StepOperands<T, C>::kPieces; ++e) {
       const int32_t blk = sizeof(T) == 2 ? st * 32 + 8 * kg + e : st * 16 + 4 * e + kg;
-      o.av[e] = s_val[blk * 16 + q];
       o.x[e] = ld.load(s_src[blk]);
     }
   };
-  auto multiply = [&](const StepOperands<T, C>& o) {
+  auto multiply = [&](const StepOperands<T, C>& o, int32_t st) {
+    lanes::raw16_t* slot = reinterpret_cast<lanes::raw16_t*>(ring + (st & 1) * 1024);
+    slot[lane] = o.v;
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    const T* sv = reinterpret_cast<const T*>(slot);
     if constexpr (sizeof(T) == 2) {
+      half8_t av;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) av[e] = sv[(8 * kg + e) * 16 + q];
 #pragma unroll
       for (int j = 0; j < C; ++j) {
         half8_t b;
 #pragma unroll
         for (int e = 0; e < 8; ++e) b[e] = o.x[e][j];
-        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(o.av, b, acc[j], 0, 0, 0);
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b, acc[j], 0, 0, 0);
       }
     } else {
+      float4_t av;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) av[e] = sv[(4 * e + kg) * 16 + q];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(o.av[u], o.x[u][j], acc[j], 0, 0, 0);
+          acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[u], o.x[u][j], acc[j], 0, 0, 0);
       }
     }
   };
   if constexpr (C == 8) {
-    // Twice the operands per step: one step in registers (two would halve
-    // the waves per SIMD).
+    // Twice the operands per step: one step in registers (a second would
+    // not fit the register budget of 4 waves per SIMD).
     for (int32_t st = 0; st < steps; ++st) {
       StepOperands<T, C> A;
       fetch(A, st);
-      multiply(A);
+      multiply(A, st);
     }
     return;
   }
@@ -309,17 +361,17 @@ __device__ inline void group_sum(const BlockArgs<T, I>& a, const uint32_t* s_src
   int32_t st = 0;
   for (; st + 3 <= steps; st += 2) {
     fetch(B, st + 1);
-    multiply(A);
+    multiply(A, st);
     fetch(A, st + 2);
-    multiply(B);
+    multiply(B, st + 1);
   }
   // A holds step st; one or two steps remain.
   if (st + 2 == steps) {
     fetch(B, st + 1);
-    multiply(A);
-    multiply(B);
+    multiply(A, st);
+    multiply(B, st + 1);
   } else {
-    multiply(A);
+    multiply(A, st);
   }
 }
 
@@ -343,12 +395,12 @@ __device__ inline unsigned window_vector_rows(const BlockArgs<T, I>& a, int64_t 
 // not depend on it); a window that fits is staged once for all column groups.
 template <typename T, typename I, int C, typename Loader, bool kS>
 __device__ inline void window_chunk(const BlockArgs<T, I>& a, int64_t s, int64_t b0, int64_t b1,
-                                    float* slot, uint32_t* s_col, T* s_val) {
+                                    float* slot, uint32_t* s_col, unsigned char* ring) {
   const int64_t n = b1 - b0;
   const bool once = n <= a.stage;
   unsigned vec = 0;
   if (once)
-    vec = stage_chunk<T, I, Loader, kS>(a, s, slot == nullptr, b0, b1, s_col, s_val);
+    vec = stage_chunk<T, I, Loader, kS>(a, s, slot == nullptr, b0, b1, s_col);
   else if (slot == nullptr)
     vec = window_vector_rows(a, s);
   constexpr int64_t kGroupCols = 16 * C;
@@ -367,13 +419,13 @@ __device__ inline void window_chunk(const BlockArgs<T, I>& a, int64_t s, int64_t
 #pragma unroll
     for (int j = 0; j < C; ++j) acc[j] = float4_t{0.f, 0.f, 0.f, 0.f};
     if (once) {
-      if (active) group_sum<T, I, C, Loader, kS>(a, s_col, s_val, n, n0, lane, acc);
+      if (active) group_sum<T, I, C, Loader, kS>(a, s_col, a.Cvalue + 16 * b0, ring, n, n0, lane, acc);
     } else {
       for (int64_t sb = 0; sb < n; sb += a.stage) {
         const int64_t m = n - sb < a.stage ? n - sb : a.stage;
         __syncthreads();  // the previous piece is no longer read
-        stage_chunk<T, I, Loader, kS>(a, s, false, b0 + sb, b0 + sb + m, s_col, s_val);
-        if (active) group_sum<T, I, C, Loader, kS>(a, s_col, s_val, m, n0, lane, acc);
+        stage_chunk<T, I, Loader, kS>(a, s, false, b0 + sb, b0 + sb + m, s_col);
+        if (active) group_sum<T, I, C, Loader, kS>(a, s_col, a.Cvalue + 16 * (b0 + sb), ring, m, n0, lane, acc);
       }
     }
     const int64_t c0 = n0 + C * q;
@@ -511,11 +563,18 @@ __device__ inline void settle_window(const BlockArgs<T, I>& a, int64_t s, int64_
 #endif
 // Waves per SIMD the register budget of block_windows is fitted to (C = 8
 // holds twice the accumulators and dense pieces).
-template <typename T, typename I, int C, typename Loader, bool kS>
+// A window that fits one staging piece (the common case) takes the lean
+// path with C-column pieces; longer windows and the overflow ranges take
+// 4-column pieces (their MFMA sequence per output element is the same, so
+// results do not depend on the path), which keeps their chunk loops and
+// partial stores out of the lean path's register budget.
+template <typename T, typename I, int C, template <typename, int> class LoaderT, bool kS>
 __global__ __launch_bounds__(64 * kMaxWaves) __attribute__((amdgpu_waves_per_eu(C == 8 ? SPMM_BLOCK_WAVES_WIDE : SPMM_BLOCK_WAVES))) void block_windows(BlockArgs<T, I> a) {
   extern __shared__ __align__(16) unsigned char smem[];
-  T* s_val = reinterpret_cast<T*>(smem);                           // [stage][16]
-  uint32_t* s_col = reinterpret_cast<uint32_t*>(smem + a.stage * 16 * sizeof(T));  // [stage]
+  // The wave's ring of A fragments (kRingBytes per wave), then the staged
+  // column sources ([stage] uint32).
+  unsigned char* ring = smem + (threadIdx.x >> 6) * kRingBytes;
+  uint32_t* s_col = reinterpret_cast<uint32_t*>(smem + (blockDim.x >> 6) * kRingBytes);
   const int64_t lead = a.per_xcd * kXcds;
   const int64_t g = blockIdx.x;
   const int64_t n16 = 16 * a.N;
@@ -543,9 +602,14 @@ __global__ __launch_bounds__(64 * kMaxWaves) __attribute__((amdgpu_waves_per_eu(
       }
       return;
     }
+    if (b1 - b0 <= a.stage) {
+      window_chunk<T, I, C, LoaderT<T, C>, kS>(a, s, b0, b1, nullptr, s_col, ring);
+      return;
+    }
     const bool single = b1 - b0 <= a.kbig;
-    window_chunk<T, I, C, Loader, kS>(a, s, b0, single ? b1 : b0 + a.kbig,
-                                  single ? nullptr : a.slots + (2 * ((b0 + a.kbig) / a.kbig) + 1) * n16, s_col, s_val);
+    window_chunk<T, I, 4, LoaderT<T, 4>, kS>(a, s, b0, single ? b1 : b0 + a.kbig,
+                                             single ? nullptr : a.slots + (2 * ((b0 + a.kbig) / a.kbig) + 1) * n16,
+                                             s_col, ring);
     if (!single) settle_window<kS>(a, s, b0, b1);
     return;
   }
@@ -565,7 +629,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) __attribute__((amdgpu_waves_per_eu(
   const int64_t lo = b0 + a.kbig > bk ? b0 + a.kbig : bk;
   const int64_t hi = b1 < bk + a.kbig ? b1 : bk + a.kbig;
   if (lo >= hi) return;
-  window_chunk<T, I, C, Loader, kS>(a, s, lo, hi, a.slots + (2 * k) * n16, s_col, s_val);
+  window_chunk<T, I, 4, LoaderT<T, 4>, kS>(a, s, lo, hi, a.slots + (2 * k) * n16, s_col, ring);
   settle_window<kS>(a, s, b0, b1);
 }
 
@@ -607,30 +671,29 @@ spmm_status block_typed(const void* Crowptr, const void* Ccol, const void* Cvalu
   a.noverflow = block_overflow_ranges(a.limit, a.kbig);
   a.cnt = reinterpret_cast<uint32_t*>(slots + a.noverflow * 2 * 16 * N);
   a.per_xcd = ceil_div(windows, kXcds * kBlockXcdRun) * kBlockXcdRun;
-  const int C = lane_cols_for<T>(N);
+  const int C = lane_cols_for<T>(N, windows);
   const int64_t groups = ceil_div(N, 16 * C);
   const int waves = groups < kMaxWaves ? static_cast<int>(groups) : kMaxWaves;
-  // Staging piece: about twice the mean window, 64 blocks up to a 20 KB LDS
-  // budget (512 blocks fp16, 256 fp32), so LDS per work-group stays small for
-  // small windows and most windows stage once.
+  // Staging piece (4 bytes of LDS per block): about twice the mean window,
+  // from 64 blocks up to the chunk, so most windows stage once and LDS per
+  // work-group stays small enough for 16 work-groups per CU.
   const int64_t mean = a.limit / windows;
-  const int64_t stage_max = sizeof(T) == 2 ? 512 : 256;
   a.stage = 64;
-  while (a.stage < 2 * mean && a.stage < a.kbig && a.stage < stage_max) a.stage *= 2;
-  const size_t stage_lds = static_cast<size_t>(a.stage) * (16 * sizeof(T) + sizeof(uint32_t));
+  while (a.stage < 2 * mean && a.stage < a.kbig) a.stage *= 2;
+  const size_t stage_lds = static_cast<size_t>(waves) * kRingBytes + static_cast<size_t>(a.stage) * sizeof(uint32_t);
   const int64_t grid = a.per_xcd * kXcds + a.noverflow;
   constexpr int kWide = sizeof(T) == 2 ? 8 : 4;  // fp32 only has C = 4
   // Dense operands within a 32-bit byte extent use buffer loads.
   const bool buffer = buffer_extent(K, ldd, N, sizeof(T)) <= kBlockBufferLimit;
   // Column passes (ldd > N) take the strided instantiations.
-  auto kernel = ldd == N ? (buffer ? (C == 8 ? block_windows<T, I, kWide, BlockBufferLoader<T, kWide>, false>
-                                            : block_windows<T, I, 4, BlockBufferLoader<T, 4>, false>)
-                                   : (C == 8 ? block_windows<T, I, kWide, BlockGlobalLoader<T, kWide>, false>
-                                             : block_windows<T, I, 4, BlockGlobalLoader<T, 4>, false>))
-                         : (buffer ? (C == 8 ? block_windows<T, I, kWide, BlockBufferLoader<T, kWide>, true>
-                                            : block_windows<T, I, 4, BlockBufferLoader<T, 4>, true>)
-                                   : (C == 8 ? block_windows<T, I, kWide, BlockGlobalLoader<T, kWide>, true>
-                                             : block_windows<T, I, 4, BlockGlobalLoader<T, 4>, true>));
+  auto kernel = ldd == N ? (buffer ? (C == 8 ? block_windows<T, I, kWide, BlockBufferLoader, false>
+                                            : block_windows<T, I, 4, BlockBufferLoader, false>)
+                                   : (C == 8 ? block_windows<T, I, kWide, BlockGlobalLoader, false>
+                                             : block_windows<T, I, 4, BlockGlobalLoader, false>))
+                         : (buffer ? (C == 8 ? block_windows<T, I, kWide, BlockBufferLoader, true>
+                                            : block_windows<T, I, 4, BlockBufferLoader, true>)
+                                   : (C == 8 ? block_windows<T, I, kWide, BlockGlobalLoader, true>
+                                             : block_windows<T, I, 4, BlockGlobalLoader, true>));
   if (zero_counts && a.noverflow > 0) {
     hipLaunchKernelGGL(block_zero_counts, dim3(static_cast<unsigned>(ceil_div(a.noverflow, 256))), dim3(256), 0,
                        stream, a.cnt, a.noverflow);
