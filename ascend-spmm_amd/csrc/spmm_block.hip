@@ -478,8 +478,16 @@ __device__ inline void settle_window(const BlockArgs<T, I>& a, int64_t s, int64_
   __shared__ uint32_t s_last;
   const int64_t k0 = (b0 + a.kbig) / a.kbig;
   const int64_t k_end = (b1 - 1) / a.kbig;
-  // This work-group's piece stores are complete (performed at agent scope)
-  // before the count that publishes them.
+  // The pieces are stored and read with agent-scope atomic accesses, which
+  // on gfx950 are performed at the device coherence point (write-through
+  // stores, loads that bypass non-coherent cache lines).  A wave's vector
+  // memory counter reaches zero only when its stores are performed, so
+  // after every wave's wait and the barrier, all of this work-group's
+  // pieces are visible to any work-group that reads the count.  Agent-scope
+  // release/acquire fences would say the same in the HIP memory model, but
+  // they write back and invalidate the whole L2 of the XCD per piece: with
+  // them config 5's graph path (thousands of pieces) took 18.9 instead of
+  // 12.2 ms.
   __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   if (threadIdx.x == 0) {

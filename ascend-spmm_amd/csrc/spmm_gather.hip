@@ -820,6 +820,10 @@ __device__ void segment_worker(const Geometry<I>& g, int64_t wid, const I* __res
     const int64_t c0 = ((p % chunks) * L + lane) * V;
     float* dst = ws + (2 * j + (wi & 1)) * slot + c0;
     const int32_t n_pos = static_cast<int32_t>(s1 - s0);
+    // segment_classify writes only non-empty segments; an empty one can come
+    // only from a word this call did not write (row pointers that do not
+    // cover [0, nnz)), and is skipped before any index is formed from it.
+    if (n_pos <= 0) continue;
     const int32_t n_pad = (n_pos + kSegGroup - 1) / kSegGroup * kSegGroup;
     const int32_t n_stage = n_pad + (kSegInflight - 1) * kSegBatch;
     // The previous pair's staging reads are done before it is overwritten.
@@ -830,8 +834,8 @@ __device__ void segment_worker(const Geometry<I>& g, int64_t wid, const I* __res
       T vs[kSegStageUnroll];
 #pragma unroll
       for (int u = 0; u < kSegStageUnroll; ++u) {
-        // Unconditional loads (clamped into the segment, n_pos >= 1 here), so
-        // no branch separates them.
+        // Unconditional loads (clamped into the segment; n_pos >= 1), so no
+        // branch separates them.
         const int32_t i = i0 + u * L + lane;
         const int64_t q = s0 + (i < n_pos ? i : n_pos - 1);
         cs[u] = col[q];

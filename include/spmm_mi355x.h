@@ -103,7 +103,11 @@ spmm_status spmm_csr_run(const spmm_csr_desc* desc,
  * whose scratch (spmm_csr_workspace's figure) exceeds it fails with
  * SPMM_ERR_CONTRACT before touching the device.  Every call on one GPU shares
  * that GPU's array, so calls that overlap on one GPU (different streams, or
- * host threads, without ordering between them) race and must not be made. */
+ * host threads, without ordering between them) race and must not be made.
+ * The first call on each device looks up the array's device address
+ * (hipGetSymbolAddress) and keeps it; make that first call outside stream
+ * capture (one eager call before capturing), so that no capture sees the
+ * lookup.  Later calls only launch kernels and may be captured. */
 size_t spmm_csr_noalloc_max_scratch(void);
 
 spmm_status spmm_csr_run_noalloc(const spmm_csr_desc* desc,

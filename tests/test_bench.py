@@ -85,6 +85,37 @@ def test_bench_preprocess_line():
     assert d["roofline"]["bound"] == "hbm" and d["value"] > 0
 
 
+def test_probe_limits_note():
+    """bench.py runs the position-order probe only within spmm_gather_probe's
+    limits (64 lanes of 16 bytes per row, a 4 GB dense operand); elsewhere
+    the line carries the reason instead of failing."""
+    sys.path.insert(0, REPO)
+    import bench
+
+    class W:
+        cols = 100000
+
+    assert bench.probe_limits_note(W, 128, 2) is None
+    assert bench.probe_limits_note(W, 512, 2) is None
+    assert "64 lanes" in bench.probe_limits_note(W, 1024, 2)
+    assert "64 lanes" in bench.probe_limits_note(W, 512, 4)
+    W.cols = 1 << 24
+    assert "4 GB" in bench.probe_limits_note(W, 256, 2)
+
+
+@pytest.mark.gpu
+def test_bench_fp32_width_512_line():
+    """A csr line at fp32 N=512 (beyond the probe's rows) still prints its
+    JSON line, with the probe fields null and the reason given."""
+    proc = run_bench("--config", "1", "--width", "512", "--steps", "2", "--warmup", "1", "--no-cpu",
+                     "--no-block-path", "--no-cold")
+    assert proc.returncode == 0, proc.stderr[-2000:]
+    d = json.loads([line for line in proc.stdout.splitlines() if line.strip()][-1])
+    r = d["roofline"]
+    assert r["position_order_probe_ms_per_call"] is None and "64 lanes" in r["position_order_probe_note"]
+    assert d["value"] > 0
+
+
 def test_traffic_table_is_keyed_to_the_kernel_sources():
     """roofline.traffic comes from the PMC table only when the entry was
     measured on the current kernel sources (their hash); otherwise it is

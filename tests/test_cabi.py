@@ -274,6 +274,56 @@ def test_rowscalar_host_validation(lib):
     assert lib.spmm_csr_rowscalar_run(ctypes.byref(d), None, None, None, None, None, None) == 1
 
 
+def test_gather_probe_host_validation(lib):
+    """spmm_gather_probe refuses, before any device call, what it cannot run:
+    int64 column ids, rows wider than 64 lanes of 16 bytes (fp16 N > 512,
+    fp32 N > 256), null and misaligned pointers."""
+    fake = ctypes.c_void_p(0x10000)  # aligned; never dereferenced: every check precedes the launch
+    probe = lib.spmm_gather_probe
+    d = CsrDesc(10, 5, 10, 128, 1, 0)
+    assert probe(ctypes.byref(d), fake, fake, fake, fake, None) == 4
+    assert b"int32 column ids only" in lib.spmm_last_error()
+    for width, value_type in ((1024, 0), (512, 1)):
+        d = CsrDesc(10, 5, 10, width, 0, value_type)
+        assert probe(ctypes.byref(d), fake, fake, fake, fake, None) == 4
+        assert b"rows wider than 64 lanes" in lib.spmm_last_error()
+    d = CsrDesc(10, 5, 10, 128, 0, 0)
+    assert probe(ctypes.byref(d), None, fake, fake, fake, None) == 1
+    assert probe(ctypes.byref(d), fake, fake, ctypes.c_void_p(0x10004), fake, None) != 0
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("value_type,N", [(0, 128), (0, 512), (1, 64), (1, 256)])
+def test_gather_probe_sums(lib, value_type, N):
+    """The probe accumulates value x dense row over every nonzero of its
+    ranges and each thread writes the sum of its lanes' columns, so the sink
+    adds up to sum_p value[p] * rowsum(dense[col[p]]) (invalid columns add
+    zero); checked against that closed form in fp64."""
+    import torch
+
+    rng = np.random.default_rng(31 + N)
+    nnz, K = 5000, 700
+    col = rng.integers(0, K, nnz).astype(np.int32)
+    col[::23] = K + 5
+    npdt = np.float16 if value_type == 0 else np.float32
+    vals = rng.uniform(-1, 1, nnz).astype(npdt)
+    B = rng.standard_normal((K, N)).astype(npdt)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    d = CsrDesc(1, nnz, K, N, 0, value_type)
+    lib.spmm_gather_probe_sink.restype = ctypes.c_size_t
+    sink = torch.full((int(lib.spmm_gather_probe_sink(ctypes.byref(d))),), float("nan"), device="cuda")
+    d_col, d_val, d_B = t(col), t(vals), t(B)
+    p = lambda x: ctypes.c_void_p(x.data_ptr())
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    assert lib.spmm_gather_probe(ctypes.byref(d), p(d_col), p(d_val), p(d_B), p(sink), stream) == 0
+    torch.cuda.synchronize()
+    keep = col < K
+    rowsum = B.astype(np.float64).sum(axis=1)
+    expected = float((vals.astype(np.float64)[keep] * rowsum[col[keep]]).sum())
+    got = float(sink.double().sum())
+    assert abs(got - expected) <= 1e-3 * max(1.0, float(np.abs(vals.astype(np.float64)[keep] * rowsum[col[keep]]).sum()))
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("value_type,N", [(0, 16), (0, 128), (1, 8), (1, 64)])
 def test_rowscalar_baseline_matches_oracle_and_csr(lib, value_type, N):
