@@ -329,19 +329,41 @@ def test_vector_path_width_invariant_bitwise(spmm_npu, dtype):
         assert torch.equal(part, full[:, :n]), f"width {n} differs"
 
 
-@pytest.mark.parametrize("dtype", ["fp16", "fp32"])
-def test_block_path_width_invariant_bitwise(spmm_npu, dtype):
+@pytest.mark.parametrize("dtype,rows", [("fp16", 320), ("fp32", 320), ("fp16", 16 * 3000), ("fp32", 16 * 3000)])
+def test_block_path_width_invariant_bitwise(spmm_npu, dtype, rows):
     """Mixed operator on a preprocess layout (block part + vector part):
     C_maxwidth[:, :n] == C_n bit for bit.  fp16 outputs of 256 columns or
-    more take 8-column lane pieces in the block kernel, narrower ones 4, so
-    this also checks that an element's MFMA sequence does not depend on
-    that choice (widths 192 and 272 end in partial column groups)."""
+    more take 8-column lane pieces in the block kernel, narrower ones 4, and
+    128 columns take 8 when there are at least 2048 block windows (the
+    3000-window matrices), so this also checks that an element's MFMA
+    sequence does not depend on that choice (widths 192 and 272 end in
+    partial column groups)."""
     rng = np.random.default_rng(23)
-    crow, col = random_csr(rng, 320, 400, 60, long_rows=[(3, 400), (170, 380)])
+    if rows == 320:
+        crow, col = random_csr(rng, 320, 400, 60, long_rows=[(3, 400), (170, 380)])
+        cols = 400
+    else:
+        # Windows of 16 rows with every row on the same 12 columns near the
+        # window's diagonal (block windows for the cost model), and a few
+        # scattered rows for the vector part.
+        cols = 4096
+        deg = np.where(rng.random(rows) < 0.97, 12, 3)
+        crow = np.zeros(rows + 1, np.int64)
+        crow[1:] = np.cumsum(deg)
+        parts = []
+        for r in range(rows):
+            if deg[r] == 12:
+                base = (r // 16 * 7) % (cols - 12)
+                parts.append(np.arange(base, base + 12))
+            else:
+                parts.append(np.sort(rng.choice(cols, 3, replace=False)))
+        col = np.concatenate(parts).astype(np.int64)
     vals = rng.uniform(-1, 1, col.size).astype(NP_DT[dtype])
     maxw = 1024 if dtype == "fp16" else 512
-    B = rng.standard_normal((400, maxw)).astype(NP_DT[dtype])
-    p = spmm_npu.preprocess(torch.from_numpy(crow), torch.from_numpy(col), torch.from_numpy(vals), 320, 400, 16)
+    B = rng.standard_normal((cols, maxw)).astype(NP_DT[dtype])
+    p = spmm_npu.preprocess(torch.from_numpy(crow), torch.from_numpy(col), torch.from_numpy(vals), rows, cols, 16)
+    if rows > 320:
+        assert p["crow_window_ptr"].numel() - 1 >= 2048
     i32 = torch.int32
     assert p["unique_col_ids"].numel() > 0 and p["vcol_indices"].numel() > 0
 
