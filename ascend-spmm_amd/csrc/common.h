@@ -171,15 +171,18 @@ int64_t block_overflow_ranges(int64_t blocks, int64_t kbig);
 // pass left in `vpart` ([16*windows][width]) for its rows with vector
 // nonzeros, rounded once.  `slots` holds the pieces of windows longer than
 // block_chunk ([ranges][2][16][width] fp32) followed by one uint32 counter per
-// range (block_counter_offset), which must be zero when the block kernel
-// starts: zeroed by the gather's post pass when it runs in the same call
-// (launch_gather's zero_counts), else by launch_block itself (zero_counts).
+// range (block_counter_offset).  `counters_zeroed`: the gather's post pass of
+// the same call zeroed the counters (launch_gather's zero_counts), and
+// overflow work-groups take the long windows' segments, counted on them;
+// otherwise each long window's own work-group sums its segments one after
+// another (the same pieces added in the same order: the same results) and
+// the counters are not used.
 spmm_status launch_block(int32_t index_type, int32_t value_type,
                          const void* Crowptr, const void* Ccol, const void* Cvalue,
                          int64_t windows, int64_t block_count, int64_t block_values,
                          const void* Vrowptr, int64_t vector_rows, int64_t vector_nnz,
                          const void* dense, int64_t dense_rows, int64_t width, int64_t ld,
                          void* out, const float* vpart, float* slots, const int32_t* order,
-                         bool zero_counts, hipStream_t stream);
+                         bool counters_zeroed, hipStream_t stream);
 
 }  // namespace spmm

@@ -37,7 +37,12 @@
 //    piece's work-group stores its fp32 sum and counts itself on the
 //    window's counter; the one that completes the count adds the pieces in
 //    order (first chunk, then the overflow ranges), so the split is
-//    deterministic and needs no combine launch.
+//    deterministic and needs no combine launch.  The counters start at zero
+//    when the gather kernels of the same call ran first (their post pass
+//    zeroes them); otherwise (a call with no vector part) the window's own
+//    work-group computes the same pieces one after another and adds them in
+//    the same order, so no counter and no zeroing launch are needed and the
+//    results are the same bit for bit.
 //  * Vector (CSR) nonzeros of rows inside block windows are summed by the CSR
 //    gather kernel first (so long rows get its load balance) and left in an
 //    fp32 workspace; the block kernel adds them after the block sum and
@@ -98,6 +103,7 @@ struct BlockArgs {
   int64_t kbig, noverflow, per_xcd;
   int64_t stage;           // blocks staged in LDS at a time (multiple of the K-step)
   int zero_empty;          // no vector part: windows without blocks write their rows as zeros
+  int serial;              // counters not zeroed: a long window's own work-group computes every piece
   const int32_t* order;    // locality order of the windows (from the gather post pass), or null
 
   __device__ inline int64_t crp(int64_t s) const { return clampi(static_cast<int64_t>(Crowptr[s]), 0, limit); }
@@ -466,36 +472,13 @@ __device__ inline void window_chunk(const BlockArgs<T, I>& a, int64_t s, int64_t
   }
 }
 
-// A window of blocks [b0, b1), longer than kbig, is summed in pieces: its own
-// work-group's first chunk (slot (k0, 1), k0 = (b0 + kbig) / kbig) and one
-// segment per overflow range k0 .. k_end (slot (k, 0)).  After storing its
-// piece, a work-group counts itself on cnt[k0]; the one that completes the
-// count adds first chunk + segments k0, k0+1, ... in order, adds the rows'
-// vector sums, rounds once and writes the window's 16 rows, then resets the
-// counter to zero for the next call.  All threads of the work-group call it.
+// Adds the pieces of window s (first chunk in slot (k0, 1), then the
+// segments of overflow ranges k0 .. k_end in slot (k, 0)) in that order,
+// plus the rows' vector sums, rounds once and writes the window's 16 rows.
+// Every piece is stored and performed before any thread of the work-group
+// calls it.
 template <bool kS, typename T, typename I>
-__device__ inline void settle_window(const BlockArgs<T, I>& a, int64_t s, int64_t b0, int64_t b1) {
-  __shared__ uint32_t s_last;
-  const int64_t k0 = (b0 + a.kbig) / a.kbig;
-  const int64_t k_end = (b1 - 1) / a.kbig;
-  // The pieces are stored and read with agent-scope atomic accesses, which
-  // on gfx950 are performed at the device coherence point (write-through
-  // stores, loads that bypass non-coherent cache lines).  A wave's vector
-  // memory counter reaches zero only when its stores are performed, so
-  // after every wave's wait and the barrier, all of this work-group's
-  // pieces are visible to any work-group that reads the count.  Agent-scope
-  // release/acquire fences would say the same in the HIP memory model, but
-  // they write back and invalidate the whole L2 of the XCD per piece: with
-  // them config 5's graph path (thousands of pieces) took 18.9 instead of
-  // 12.2 ms.
-  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const uint32_t old = __hip_atomic_fetch_add(a.cnt + k0, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = static_cast<int64_t>(old) + 1 == k_end - k0 + 2 ? 1u : 0u;
-  }
-  __syncthreads();
-  if (!s_last) return;
+__device__ inline void combine_window(const BlockArgs<T, I>& a, int64_t s, int64_t k0, int64_t k_end) {
   const int64_t n = 16 * a.N;
   auto load4 = [](const float* p) {
     lanes::float4_t f;
@@ -554,7 +537,44 @@ __device__ inline void settle_window(const BlockArgs<T, I>& a, int64_t s, int64_
       for (int e = 0; e < 4; ++e) dst[e] = static_cast<T>(v[e]);
     }
   }
-  if (threadIdx.x == 0) __hip_atomic_store(a.cnt + k0, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// A window of blocks [b0, b1), longer than kbig, is summed in pieces: its own
+// work-group's first chunk (slot (k0, 1), k0 = (b0 + kbig) / kbig) and one
+// segment per overflow range k0 .. k_end (slot (k, 0)).  After storing its
+// piece, a work-group counts itself on cnt[k0]; the one that completes the
+// count adds first chunk + segments k0, k0+1, ... in order, adds the rows'
+// vector sums, rounds once and writes the window's 16 rows, then resets the
+// counter to zero for the next call.  With a.serial the window's own
+// work-group has stored every piece and adds them without a counter.  All
+// threads of the work-group call it.
+template <bool kS, typename T, typename I>
+__device__ inline void settle_window(const BlockArgs<T, I>& a, int64_t s, int64_t b0, int64_t b1) {
+  __shared__ uint32_t s_last;
+  const int64_t k0 = (b0 + a.kbig) / a.kbig;
+  const int64_t k_end = (b1 - 1) / a.kbig;
+  // The pieces are stored and read with agent-scope atomic accesses, which
+  // on gfx950 are performed at the device coherence point (write-through
+  // stores, loads that bypass non-coherent cache lines).  A wave's vector
+  // memory counter reaches zero only when its stores are performed, so
+  // after every wave's wait and the barrier, all of this work-group's
+  // pieces are visible to any work-group that reads the count.  Agent-scope
+  // release/acquire fences would say the same in the HIP memory model, but
+  // they write back and invalidate the whole L2 of the XCD per piece: with
+  // them config 5's graph path (thousands of pieces) took 18.9 instead of
+  // 12.2 ms.
+  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (!a.serial) {
+    if (threadIdx.x == 0) {
+      const uint32_t old = __hip_atomic_fetch_add(a.cnt + k0, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_last = static_cast<int64_t>(old) + 1 == k_end - k0 + 2 ? 1u : 0u;
+    }
+    __syncthreads();
+    if (!s_last) return;
+  }
+  combine_window<kS>(a, s, k0, k_end);
+  if (!a.serial && threadIdx.x == 0) __hip_atomic_store(a.cnt + k0, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Work-groups [0, 8*per_xcd): window s (XCD-aware runs) computes its first
@@ -615,9 +635,19 @@ __global__ __launch_bounds__(64 * kMaxWaves) __attribute__((amdgpu_waves_per_eu(
       return;
     }
     const bool single = b1 - b0 <= a.kbig;
-    window_chunk<T, I, 4, LoaderT<T, 4>, kS>(a, s, b0, single ? b1 : b0 + a.kbig,
-                                             single ? nullptr : a.slots + (2 * ((b0 + a.kbig) / a.kbig) + 1) * n16,
-                                             s_col, ring);
+    const int64_t k0 = (b0 + a.kbig) / a.kbig;
+    // Piece k0 - 1 is the first chunk.  With a.serial, the same work-group
+    // then sums the segment of every overflow range k = k0 .. (b1 - 1) / kbig
+    // into slot (k, 0): the blocks an overflow work-group would take.
+    const int64_t k_last = single || !a.serial ? k0 - 1 : (b1 - 1) / a.kbig;
+    for (int64_t k = k0 - 1; k <= k_last; ++k) {
+      if (k >= k0) __syncthreads();  // the previous piece's staged columns are no longer read
+      const int64_t bk = k * a.kbig;
+      const int64_t lo = k < k0 ? b0 : (b0 + a.kbig > bk ? b0 + a.kbig : bk);
+      const int64_t hi = k < k0 ? (single ? b1 : b0 + a.kbig) : (b1 < bk + a.kbig ? b1 : bk + a.kbig);
+      float* const slot = single ? nullptr : a.slots + (k < k0 ? 2 * k0 + 1 : 2 * k) * n16;
+      window_chunk<T, I, 4, LoaderT<T, 4>, kS>(a, s, lo, hi, slot, s_col, ring);
+    }
     if (!single) settle_window<kS>(a, s, b0, b1);
     return;
   }
@@ -641,18 +671,12 @@ __global__ __launch_bounds__(64 * kMaxWaves) __attribute__((amdgpu_waves_per_eu(
   settle_window<kS>(a, s, b0, b1);
 }
 
-// Zeroes the window counters when no earlier kernel of the call did.
-__global__ __launch_bounds__(256) void block_zero_counts(uint32_t* cnt, int64_t n) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i < n) cnt[i] = 0u;
-}
-
 template <typename T, typename I>
 spmm_status block_typed(const void* Crowptr, const void* Ccol, const void* Cvalue, int64_t windows,
                         int64_t block_count, int64_t block_values, const void* Vrowptr,
                         int64_t vector_rows, int64_t vector_nnz, const void* dense, int64_t K,
                         int64_t N, int64_t ldd, void* out, const float* vpart, float* slots, const int32_t* order,
-                        bool zero_counts, hipStream_t stream) {
+                        bool counters_zeroed, hipStream_t stream) {
   if (windows <= 0) return SPMM_OK;
   if (K > static_cast<int64_t>(kBadCol) - 1)
     return fail(SPMM_ERR_CONTRACT, "dense has too many rows for 32-bit column ids");
@@ -675,6 +699,7 @@ spmm_status block_typed(const void* Crowptr, const void* Ccol, const void* Cvalu
   a.slots = slots;
   a.zero_empty = vector_nnz == 0 ? 1 : 0;
   a.order = order;
+  a.serial = counters_zeroed ? 0 : 1;
   a.kbig = block_chunk_for(sizeof(T) == 2 ? SPMM_VALUE_F16 : SPMM_VALUE_F32, a.limit);
   a.noverflow = block_overflow_ranges(a.limit, a.kbig);
   a.cnt = reinterpret_cast<uint32_t*>(slots + a.noverflow * 2 * 16 * N);
@@ -689,7 +714,9 @@ spmm_status block_typed(const void* Crowptr, const void* Ccol, const void* Cvalu
   a.stage = 64;
   while (a.stage < 2 * mean && a.stage < a.kbig) a.stage *= 2;
   const size_t stage_lds = static_cast<size_t>(waves) * kRingBytes + static_cast<size_t>(a.stage) * sizeof(uint32_t);
-  const int64_t grid = a.per_xcd * kXcds + a.noverflow;
+  // Overflow work-groups only where the counters were zeroed (else each long
+  // window's own work-group takes its overflow segments).
+  const int64_t grid = a.per_xcd * kXcds + (a.serial ? 0 : a.noverflow);
   constexpr int kWide = sizeof(T) == 2 ? 8 : 4;  // fp32 only has C = 4
   // Dense operands within a 32-bit byte extent use buffer loads.
   const bool buffer = buffer_extent(K, ldd, N, sizeof(T)) <= kBlockBufferLimit;
@@ -702,11 +729,6 @@ spmm_status block_typed(const void* Crowptr, const void* Ccol, const void* Cvalu
                                             : block_windows<T, I, 4, BlockBufferLoader, true>)
                                    : (C == 8 ? block_windows<T, I, kWide, BlockGlobalLoader, true>
                                              : block_windows<T, I, 4, BlockGlobalLoader, true>));
-  if (zero_counts && a.noverflow > 0) {
-    hipLaunchKernelGGL(block_zero_counts, dim3(static_cast<unsigned>(ceil_div(a.noverflow, 256))), dim3(256), 0,
-                       stream, a.cnt, a.noverflow);
-    if (spmm_status st = check_launch("block_zero_counts")) return st;
-  }
   hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(grid)), dim3(64 * waves), stage_lds, stream, a);
   return check_launch("block_windows");
 }
@@ -722,11 +744,11 @@ spmm_status launch_block(int32_t index_type, int32_t value_type, const void* Cro
                          int64_t block_count, int64_t block_values, const void* Vrowptr,
                          int64_t vector_rows, int64_t vector_nnz, const void* dense,
                          int64_t dense_rows, int64_t width, int64_t ld, void* out, const float* vpart,
-                         float* slots, const int32_t* order, bool zero_counts, hipStream_t stream) {
+                         float* slots, const int32_t* order, bool counters_zeroed, hipStream_t stream) {
 #define SPMM_BLOCK_CALL(T, I)                                                                   \
   return block_typed<T, I>(Crowptr, Ccol, Cvalue, windows, block_count, block_values, Vrowptr, \
                            vector_rows, vector_nnz, dense, dense_rows, width, ld, out, vpart, slots, \
-                           order, zero_counts, stream)
+                           order, counters_zeroed, stream)
   if (value_type == SPMM_VALUE_F16) {
     if (index_type == SPMM_INDEX_I32) SPMM_BLOCK_CALL(_Float16, int32_t);
     SPMM_BLOCK_CALL(_Float16, int64_t);

@@ -307,9 +307,10 @@ spmm_status spmm_mixed_run(const spmm_mixed_desc* d, const void* Crowptr, const 
   // blocks itself, and the vector pass only covers rows past the windows.
   // With the window order (block_order_wanted), the vector pass's kernel also
   // writes the block windows' locality order, which the block kernel follows.
-  // The block kernel's window counters (after the pieces in `slots`) start
-  // at zero: the gather's post pass zeroes them when it runs (it always does
-  // when the gather covers any row), else the block launch does.
+  // The block kernel's window counters (after the pieces in `slots`) are
+  // zeroed by the gather's post pass when it runs (it always does when the
+  // gather covers any row); without it, the block kernel sums each long
+  // window's pieces in the window's own work-group and uses no counter.
   const int64_t row_lo = d->vector_nnz == 0 ? 16 * d->block_windows : 0;
   const bool gather_runs = out_rows > row_lo;
   // A dense operand much larger than the Infinity Cache is swept in column
@@ -326,7 +327,7 @@ spmm_status spmm_mixed_run(const spmm_mixed_desc* d, const void* Crowptr, const 
     if (st != SPMM_OK) return st;
     st = launch_block(d->index_type, d->value_type, Crowptr, Ccol, Cvalue, d->block_windows, d->block_count,
                       d->block_values, Vrowptr, d->vector_rows, d->vector_nnz, dense_c, d->dense_rows, lay.w,
-                      d->width, out_c, vpart, slots, order, !gather_runs, s);
+                      d->width, out_c, vpart, slots, order, gather_runs, s);
     if (st != SPMM_OK) return st;
   }
   return SPMM_OK;

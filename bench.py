@@ -66,7 +66,7 @@ OP_KERNELS = {
             "gather_tiles' segment work-groups only for inputs of at least 2^20 nonzeros and a dense "
             "operand of at most 128 MiB)"),
     "mixed-empty": "gather_tiles + gather_post (spmm_ascend_cube, empty block part)",
-    "bcsr": "block_windows (+ block_zero_counts when windows can overflow)",
+    "bcsr": "block_windows",
     "mixed": "gather_tiles + gather_post + block_windows",
     "graph": ("fill_minus_one + scatter_inverse + gather_rows (pack) + gather_tiles + gather_post + "
               "block_windows + gather_rows (restore)"),

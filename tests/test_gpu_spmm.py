@@ -836,11 +836,22 @@ def test_windows_longer_than_the_block_chunk(spmm_npu, dtype, width):
     b = O.csr_to_bcsr(crow, col, vals, rows, K, 16)
     nblk = np.diff(b["crow_window_ptr"])
     assert nblk.max() > 4096  # longer than any chunk for this block count
-    out = spmm_npu.spmm_ascend_cube(dev(b["crow_window_ptr"], i32), dev(b["unique_col_ids"], i32),
-                                    dev(b["value"]), zero_start(1), torch.zeros(0, dtype=i32, device="cuda"),
-                                    torch.zeros(0, dtype=dev(vals).dtype, device="cuda"), dev(B),
-                                    dev(O.make_start(b["crow_window_ptr"], 20)), zero_start(40))
+    bops = (dev(b["crow_window_ptr"], i32), dev(b["unique_col_ids"], i32), dev(b["value"]))
+    bstart = dev(O.make_start(b["crow_window_ptr"], 20))
+    out = spmm_npu.spmm_ascend_cube(*bops, zero_start(1), torch.zeros(0, dtype=i32, device="cuda"),
+                                    torch.zeros(0, dtype=dev(vals).dtype, device="cuda"), dev(B), bstart,
+                                    zero_start(40))
     assert_close(out[:rows], expected, dtype)
+    # Without a vector part no gather pass runs, and each long window's own
+    # work-group sums its overflow segments; with one (a single nonzero in
+    # row 0) the gather's post pass zeroes the window counters and overflow
+    # work-groups take the segments.  The long windows' rows agree bit for bit.
+    vrow = np.ones(rows + 1, np.int64)
+    vrow[0] = 0
+    out_v = spmm_npu.spmm_ascend_cube(*bops, dev(vrow, i32), torch.zeros(1, dtype=i32, device="cuda"),
+                                      dev(np.ones(1, NP_DT[dtype])), dev(B), bstart, dev(O.make_start(vrow, 40)))
+    assert torch.equal(out_v[16:rows], out[16:rows])
+    assert not torch.equal(out_v[0], out[0])
     # the same windows with part of every row in the vector part (vpart handed to the combine)
     h = O.block_level_split(crow, col, vals, rows, K, 1.0, 16)
     assert h["vcol_indices"].size > 0 and np.diff(h["crow_window_ptr"]).max() > 4096
