@@ -97,9 +97,11 @@ def pack_node_tensor(tensor, inv_permutation, packed_rows=None):
     index = inv_permutation.to(device=tensor.device, dtype=torch.long).reshape(-1)
     if tensor.size(0) != index.numel():
         raise ValueError("inv_permutation must contain one entry per original node")
-    if index.numel() and bool((index < 0).any().item()):
+    # One reduction and one read-back for both checks.
+    lowest, highest = torch.stack(torch.aminmax(index)).tolist() if index.numel() else (0, -1)
+    if lowest < 0:
         raise ValueError("inv_permutation does not map every original node")
-    minimum_rows = int(index.max().item()) + 1 if index.numel() else 0
+    minimum_rows = highest + 1
     if packed_rows is None:
         packed_rows = minimum_rows
     elif torch.is_tensor(packed_rows):
@@ -120,10 +122,8 @@ def restore_node_tensor(packed_tensor, inv_permutation):
     if packed_tensor.ndim < 1:
         raise ValueError("a packed node tensor must have at least one dimension")
     index = inv_permutation.to(device=packed_tensor.device, dtype=torch.long).reshape(-1)
-    if index.numel() and (
-        bool((index < 0).any().item())
-        or int(index.max().item()) >= packed_tensor.size(0)
-    ):
+    lowest, highest = torch.stack(torch.aminmax(index)).tolist() if index.numel() else (0, -1)
+    if lowest < 0 or highest >= packed_tensor.size(0):
         raise ValueError("inv_permutation contains an invalid packed node id")
     return _RestoreRows.apply(packed_tensor, index.contiguous())
 

@@ -96,6 +96,74 @@ def test_spmm_csr_long_rows_cross_ranges(spmm_npu, index_dtype):
     assert_close(out, O.spmm_f64(crow, col, vals, B), "fp32")
 
 
+def _gather_range(nnz):
+    """R of the CSR gather path: the largest power of two in [16, 256] with
+    2 * R * 12288 <= nnz (nnz alone decides it)."""
+    r = 16
+    while r < 256 and 2 * r * 12288 <= nnz:
+        r *= 2
+    return r
+
+
+def _piece_rows(crow, R):
+    """Row pointer whose rows are the pieces a row is summed in: the whole
+    row when it holds at most short_max(R) nonzeros (R/2, or R when R <= 32)
+    or stays inside one range of R positions; else cut at the range ends
+    (multiples of R).  Also returns each piece's source row."""
+    short = R if R <= 32 else R // 2
+    bounds, owner = [0], []
+    for r in range(crow.size - 1):
+        a, b = int(crow[r]), int(crow[r + 1])
+        cuts = [a]
+        if b - a > short and b > (a // R + 1) * R:
+            cuts += list(range((a // R + 1) * R, b, R))
+        cuts.append(b)
+        for lo, hi in zip(cuts[:-1], cuts[1:]):
+            bounds.append(hi)
+            owner.append(r)
+    return np.asarray(bounds, np.int64), np.asarray(owner, np.int64)
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "fp32"])
+@pytest.mark.parametrize("nnz_target", [300_000, 600_000, 900_000])
+def test_csr_pieces_bitwise(spmm_npu, dtype, nnz_target):
+    """Every row is the fp32 sum of its pieces (each a sequential FMA sum
+    from zero, cut at multiples of R when the row is longer than
+    short_max(R) and crosses a range end), added in order and rounded once.
+    The pieces' own sums come from spmm_csr in fp32 on a matrix whose rows
+    are the pieces (same positions, so the same R, and no piece is cut
+    again); fp16 values and dense rows are exact in fp32.  R = 16, 32 and
+    64, with rows around R and 2R and rows over several tiles."""
+    rng = np.random.default_rng(nnz_target // 1000)
+    K, width = 3000, 64
+    rows = nnz_target // 10
+    deg = rng.integers(0, 20, size=rows)
+    deg[rng.random(rows) < 0.1] = 0
+    # rows around R and 2R, and long rows over several ranges and work-groups
+    R = _gather_range(int(deg.sum()) + 40_000)
+    for r, d in [(5, R), (6, R + 1), (7, 2 * R - 1), (8, 2 * R), (9, 2 * R + 1), (100, 3 * R + 5), (101, 700),
+                 (rows // 2, 2900), (rows - 3, 1500), (rows - 1, 2 * R)]:
+        deg[r] = d
+    deg[rng.integers(0, rows, size=400)] = rng.integers(R // 2, 3 * R, size=400)
+    parts = [np.sort(rng.choice(K, int(d), replace=False)) for d in deg]
+    crow = np.zeros(rows + 1, np.int64)
+    crow[1:] = np.cumsum(deg)
+    col = np.concatenate(parts).astype(np.int64)
+    assert _gather_range(col.size) == R
+    vals = rng.uniform(-1, 1, col.size).astype(NP_DT[dtype])
+    B = rng.standard_normal((K, width)).astype(NP_DT[dtype])
+    out = run_csr(spmm_npu, crow, col, vals, B).cpu().numpy()
+    pcrow, owner = _piece_rows(crow, R)
+    pieces = run_csr(spmm_npu, pcrow, col, vals.astype(np.float32), B.astype(np.float32)).cpu().numpy()
+    expected = np.zeros((rows, width), np.float32)
+    first = np.ones(rows, bool)
+    for p, r in enumerate(owner):
+        expected[r] = pieces[p] if first[r] else expected[r] + pieces[p]
+        first[r] = False
+    assert np.array_equal(out.view(np.uint16 if dtype == "fp16" else np.uint32),
+                          expected.astype(NP_DT[dtype]).view(np.uint16 if dtype == "fp16" else np.uint32))
+
+
 def _wide_row_matrix(rng, cols):
     """About 1.13M nonzeros (above the segment workers' 2^20 threshold): one
     row of 110k columns (its ranges sweep a chunk inside one column slab, so
