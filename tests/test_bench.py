@@ -143,7 +143,8 @@ def test_traffic_table_matches_its_profiles():
     """Every entry of the PMC table names a committed profile that records
     the same kernel-sources hash and whose per-kernel FETCH_SIZE and
     WRITE_SIZE columns sum to the entry's figures (spmm:: kernels of the op,
-    the probe excluded)."""
+    the probe excluded; weighted by the dispatches per call where the table
+    gives them, as for the graph op's column passes)."""
     import re
 
     sys.path.insert(0, REPO)
@@ -152,8 +153,10 @@ def test_traffic_table_matches_its_profiles():
     for key, e in bench.PMC_KIB.items():
         text = open(os.path.join(REPO, e["profile"])).read()
         assert f"Kernel sources of the run: {e['sources']}" in text, key
+        per_call = "| dispatches per call |" in text
         fetch = write = 0.0
-        for row in re.findall(r"^\| `spmm::[^`]*` \| \d+ \| ([\d.]+) \| ([\d.]+) \|", text, flags=re.M):
-            fetch += float(row[0])
-            write += float(row[1])
+        for row in re.findall(r"^\| `spmm::[^`]*` \| (\d+) \| ([\d.]+) \| ([\d.]+) \|", text, flags=re.M):
+            k = int(row[0]) if per_call else 1
+            fetch += k * float(row[1])
+            write += k * float(row[2])
         assert abs(fetch - e["fetch_kib"]) < 0.5 and abs(write - e["write_kib"]) < 0.5, key
