@@ -12,28 +12,31 @@
 //  * Dense gather without an LDS transpose: lane (q = lane % 16, kg = lane / 16)
 //    loads, for each of its K-step blocks, C consecutive columns
 //    n0 + C*q .. n0 + C*q + C-1 of the block's dense row in one load (fp16:
-//    C = 4, 8 bytes, or C = 8, 16 bytes, for outputs of 256 columns or more;
-//    fp32: C = 4, 16 bytes).  MFMA j (j < C) takes element j of each load, so
+//    C = 4, 8 bytes, or C = 8, 16 bytes, for outputs of 256 columns or more
+//    and of 128 columns on grids of many windows, lane_cols_for; fp32: C = 4,
+//    16 bytes).  MFMA j (j < C) takes element j of each load, so
 //    its B column q is the dense column n0 + C*q + j.  C MFMAs therefore
 //    cover a column group of 16*C columns and the accumulator lane holds C
 //    consecutive output columns.  An output element's MFMA sequence is the
 //    same for either C.
-//  * A work-group first stages its chunk's block columns and values in LDS
-//    (coalesced 16-byte loads); the A fragment A[r][k] = Cvalue[16*(b0+k) + r]
-//    is then read from LDS in the [block][row] layout the reference's
-//    converters produce.  Dense pieces are raw buffer loads whose range
-//    check turns an invalid or padding block into zeros (no branches; dense
-//    operands past 4 GB use 64-bit global loads with selects).  With C = 4
-//    the next K-step's loads are issued before the current step's MFMAs, and
-//    the accumulators are finished (plus the vector sums, rounded once)
-//    straight from registers.
+//  * A work-group first stages its chunk's block sources (each block's dense
+//    row offset) in LDS.  The block values stream from memory one K-step at
+//    a time beside the dense pieces, and pass through a per-wave LDS ring
+//    from which the A fragment A[r][k] = Cvalue[16*(b0+k) + r] is read in
+//    the [block][row] layout the reference's converters produce.  Dense
+//    pieces are raw buffer loads whose range check turns an invalid or
+//    padding block into zeros (no branches; dense operands past 4 GB use
+//    64-bit global loads with selects).  With C = 4 the next K-step's loads
+//    are issued before the current step's MFMAs, and the accumulators are
+//    finished (plus the vector sums, rounded once) straight from registers.
 //  * Waves of the work-group take column groups round-robin; each group
 //    runs the whole K loop, so every output element sees the same MFMA
 //    sequence for every width N.
 //  * Windows longer than a chunk (block_chunk_for: 2048 blocks fp16, 1024
 //    fp32, growing with the total block count) are cut at fixed block
-//    positions: the window's own work-group takes its first chunk, and "overflow" work-groups take the rest in fixed
-//    global block ranges (only one window can overflow into a range).  Each
+//    positions: the window's own work-group takes its first chunk, and
+//    "overflow" work-groups take the rest in fixed global block ranges (only
+//    one window can overflow into a range).  Each
 //    piece's work-group stores its fp32 sum and counts itself on the
 //    window's counter; the one that completes the count adds the pieces in
 //    order (first chunk, then the overflow ranges), so the split is
