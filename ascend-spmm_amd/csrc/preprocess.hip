@@ -550,19 +550,18 @@ struct TaskState {
   unsigned long long best_q;     // first q with that cost
   int64_t bwin, bblocks, prefix_blocks, remaining, wnnz_b, baic, shared, naic;
   int64_t aic_real, out_rows, real_extent, layout;
-  int64_t n_aic_blocks, vnnz;
+  int64_t n_aic_blocks, vnnz, err_bits;
   double est_aic, est_aiv, est_max;
 };
 
-// The AIC block count, the vector nonzero count and the error bits, read
-// back with the task state in two copies.
-__global__ void collect_taskmap(const TaskState* __restrict__ st, const int64_t* __restrict__ slot_ptr,
-                                const int64_t* __restrict__ vrow64, const int* __restrict__ err,
-                                int64_t* __restrict__ scal) {
+// The AIC block count, the vector nonzero count and the error bits, stored in
+// the task state, which is then read back in one copy.
+__global__ void collect_taskmap(TaskState* __restrict__ st, const int64_t* __restrict__ slot_ptr,
+                                const int64_t* __restrict__ vrow64, const int* __restrict__ err) {
   if (blockIdx.x == 0 && threadIdx.x == 0) {
-    scal[0] = slot_ptr[st->naic];
-    scal[1] = vrow64[st->out_rows];
-    scal[2] = *err;
+    st->n_aic_blocks = slot_ptr[st->naic];
+    st->vnnz = vrow64[st->out_rows];
+    st->err_bits = *err;
   }
 }
 
@@ -1453,15 +1452,13 @@ spmm_status task_plan(const Csr& c, bool graph_layout, void* ws, size_t ws_bytes
   if (hipError_t e = x.prims.exclusive_sum(A.ocnt, A.vrow64, A.max_rows + 1)) return check_hip(e, "vrow scan");
   if (spmm_status st = check_launch("taskmapping")) return st;
 
-  hipLaunchKernelGGL(collect_taskmap, dim3(1), dim3(64), 0, s, A.st, A.slot_ptr, A.vrow64, S.err, S.scal);
+  hipLaunchKernelGGL(collect_taskmap, dim3(1), dim3(64), 0, s, A.st, A.slot_ptr, A.vrow64, S.err);
   TaskState hs;
   if (spmm_status st = read_back(&hs, A.st, 1, s)) return st;
-  int64_t v[3] = {0, 0, 0};
-  if (spmm_status st = read_back(v, S.scal, 3, s)) return st;
-  if (v[2] & kBadOccupancy)
+  if (hs.err_bits & kBadOccupancy)
     return fail(SPMM_ERR_INVALID_ARGUMENT,
                 "block occupancy must be in [1, window_size]; coalesce duplicate CSR entries");
-  const int64_t aic_blocks = v[0], vnnz = v[1];
+  const int64_t aic_blocks = hs.n_aic_blocks, vnnz = hs.vnnz;
 
   spmm_taskmap_info r{};
   r.aic_windows = hs.naic;
