@@ -544,6 +544,14 @@ __global__ void boundary_search(const int64_t* __restrict__ snb, const int64_t* 
 }
 
 // Scalars shared by the taskmapping kernels (device resident).
+// Host values a plan hands to its fill, kept at the head of the workspace.
+struct Header {
+  int64_t magic;
+  int64_t p_begin, n, nb;
+  int64_t a0, a1, a2, a3;  // pipeline-specific
+};
+constexpr int64_t kMagic = 0x5350'4d4d'5052'4531LL;
+
 struct TaskState {
   unsigned long long bpos;       // marginal sorted position, or ~0 (none)
   unsigned long long best_bits;  // min max-cost bits
@@ -555,13 +563,21 @@ struct TaskState {
 };
 
 // The AIC block count, the vector nonzero count and the error bits, stored in
-// the task state, which is then read back in one copy.
+// the task state, which is then read back in one copy; and the plan's header
+// for the fill (h holds the values the host already has), written before that
+// read-back so that its synchronisation covers it.
 __global__ void collect_taskmap(TaskState* __restrict__ st, const int64_t* __restrict__ slot_ptr,
-                                const int64_t* __restrict__ vrow64, const int* __restrict__ err) {
+                                const int64_t* __restrict__ vrow64, const int* __restrict__ err,
+                                Header* __restrict__ header, Header h) {
   if (blockIdx.x == 0 && threadIdx.x == 0) {
     st->n_aic_blocks = slot_ptr[st->naic];
     st->vnnz = vrow64[st->out_rows];
     st->err_bits = *err;
+    h.a0 = st->n_aic_blocks;
+    h.a1 = st->vnnz;
+    h.a2 = st->out_rows;
+    h.a3 = st->naic;
+    *header = h;
   }
 }
 
@@ -942,13 +958,6 @@ Csr from_matrix(const spmm_csr_matrix* m) {
   return Csr{m->rows, m->cols, m->nnz, m->index_type, m->value_type, m->rowptr, m->col, m->value};
 }
 
-// Host values a plan hands to its fill, kept at the head of the workspace.
-struct Header {
-  int64_t magic;
-  int64_t p_begin, n, nb;
-  int64_t a0, a1, a2, a3;  // pipeline-specific
-};
-constexpr int64_t kMagic = 0x5350'4d4d'5052'4531LL;
 
 // Arrays of the window sort (upper bounds from the sizes only).
 struct WinSort {
@@ -1452,7 +1461,8 @@ spmm_status task_plan(const Csr& c, bool graph_layout, void* ws, size_t ws_bytes
   if (hipError_t e = x.prims.exclusive_sum(A.ocnt, A.vrow64, A.max_rows + 1)) return check_hip(e, "vrow scan");
   if (spmm_status st = check_launch("taskmapping")) return st;
 
-  hipLaunchKernelGGL(collect_taskmap, dim3(1), dim3(64), 0, s, A.st, A.slot_ptr, A.vrow64, S.err);
+  hipLaunchKernelGGL(collect_taskmap, dim3(1), dim3(64), 0, s, A.st, A.slot_ptr, A.vrow64, S.err, x.header,
+                     Header{kMagic, S.p_begin, n, nb, 0, 0, 0, 0});
   TaskState hs;
   if (spmm_status st = read_back(&hs, A.st, 1, s)) return st;
   if (hs.err_bits & kBadOccupancy)
@@ -1474,7 +1484,6 @@ spmm_status task_plan(const Csr& c, bool graph_layout, void* ws, size_t ws_bytes
   r.estimated_aiv_cost = hs.est_aiv;
   r.estimated_max_cost = hs.est_max;
 
-  Header h{kMagic, S.p_begin, n, nb, aic_blocks, vnnz, hs.out_rows, hs.naic};
   if (layout) {
     // P * A^T * P^T: entry (r, c) goes to row inv[c], column inv[r], in
     // (row, position) order (packed_column_reindex.h:43-101), then the fixed
@@ -1506,12 +1515,10 @@ spmm_status task_plan(const Csr& c, bool graph_layout, void* ws, size_t ws_bytes
     r.t_vector_nnz = tv;
   }
   *info = r;
-  // Persist: the plan header plus the transpose split's sizes.
-  Header ht{kMagic, layout ? A.T.S.p_begin : 0, layout ? A.T.S.n : 0, layout ? A.T.S.nb : 0, r.t_blocks,
-            r.t_vector_nnz, 0, 0};
-  hipError_t e = hipMemcpyAsync(x.header, &h, sizeof h, hipMemcpyHostToDevice, s);
-  if (e == hipSuccess && layout)
-    e = hipMemcpyAsync(A.theader, &ht, sizeof ht, hipMemcpyHostToDevice, s);
+  if (!layout) return SPMM_OK;  // collect_taskmap stored the plan header
+  // The transpose split's sizes beside it.
+  Header ht{kMagic, A.T.S.p_begin, A.T.S.n, A.T.S.nb, r.t_blocks, r.t_vector_nnz, 0, 0};
+  hipError_t e = hipMemcpyAsync(A.theader, &ht, sizeof ht, hipMemcpyHostToDevice, s);
   if (e == hipSuccess) e = hipStreamSynchronize(s);
   return check_hip(e, "storing the plan");
 }
