@@ -20,10 +20,12 @@
 //    share an L2).  It stages the tile's nonzeros in LDS in one round of
 //    loads: per position the byte offset of its dense row (or a sentinel
 //    past the dense operand for an invalid column), the value bits, and a
-//    row-end mark.  Each wavefront finds the row holding the tile's first
-//    position by a multiway search over rowptr, overlapping the staging
-//    loads; the work-group then marks the last position of every row that
-//    ends in the tile.  Each lane group streams its range in order: batches
+//    row-end mark.  Wavefront 0 finds the row holding the tile's first
+//    position by a multiway search over rowptr while the others stage (or
+//    every wavefront does, overlapping its staging loads, when the tile
+//    needs all of them to stage in one round); the work-group then marks the
+//    last position of every row that ends in the tile.  Each lane group
+//    streams its range in order: batches
 //    of 4 positions, two in flight, each position one raw buffer load of
 //    16 bytes per lane (the buffer range check returns zeros for the
 //    sentinel, so no position needs address arithmetic or a select), fp32
@@ -963,9 +965,8 @@ __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(kSeg
 
   // Stage the tile's nonzeros (positions clamped to [0, nnz); those outside
   // our rows are never read): loader source per column (checked against K
-  // once here), value bits (-0 for an invalid column), marks cleared.  The
-  // first chunk's loads are issued before the row search below, so the two
-  // overlap.
+  // once here), value bits (-0 for an invalid column), marks cleared, while
+  // the row search below runs.
   const int64_t nr = j1 - j0;
   if (threadIdx.x <= nr) {
     s_cut[threadIdx.x] = -1;
@@ -973,48 +974,62 @@ __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(kSeg
   }
   // rS: the row holding position P0 (tiles starting outside our positions
   // [base, end) clamp to the row range); runs of empty rows before the tile
-  // are skipped.  Every wavefront finds it by the same search, or (kSeg)
-  // reads it from tile_row, clamped to the row range (row pointers that
-  // decrease leave entries unwritten).
+  // are skipped.  It comes from a row search (or, kSeg, from tile_row,
+  // clamped to the row range: row pointers that decrease leave entries
+  // unwritten).  The search runs in wavefront 0 alone while the other
+  // wavefronts stage, when they can stage the tile in one round: its probes
+  // then do not wait behind staging loads of its own (loads return in order).
+  // Otherwise every wavefront runs it, overlapping its own staging loads.
   int64_t rS = g.row_hi;
   if constexpr (kSeg)
     rS = P0 < base ? g.row_lo : (P0 < end ? clampi(g.tile_row[tile], g.row_lo, g.row_hi - 1) : g.row_hi);
-  // The tile's positions from a work-group-uniform base (P0 < nnz), 32-bit
-  // offsets clamped to the last position.
-  const I* __restrict__ col_t = col + P0;
-  const T* __restrict__ value_t = value + P0;
-  const uint32_t last = static_cast<uint32_t>(g.nnz - 1 - P0);
-  for (int64_t i0 = 0; i0 < tile_positions; i0 += kStageUnroll * blockDim.x) {
-    I cs[kStageUnroll];
-    T vs[kStageUnroll];
-    // The block size through an empty asm: offsets recomputed per round
-    // rather than hoisted out of the loop (where they would hold kStageUnroll
-    // address registers each and spill).
-    uint32_t bd = blockDim.x;
-    __asm__ volatile("" : "+s"(bd));
+  const bool search_wave = !kSeg && blockDim.x >= 128 &&
+                           tile_positions <= kStageUnroll * static_cast<int64_t>(blockDim.x - 64);
+  __shared__ int64_t s_rS;
+  if (search_wave && threadIdx.x < 64) {
+    rS = P0 < base ? g.row_lo : (P0 < end ? find_row(g, P0, base, end) : g.row_hi);
+    if (threadIdx.x == 0) s_rS = rS;
+  } else {
+    // The tile's positions from a work-group-uniform base (P0 < nnz), 32-bit
+    // offsets clamped to the last position.
+    const I* __restrict__ col_t = col + P0;
+    const T* __restrict__ value_t = value + P0;
+    const uint32_t last = static_cast<uint32_t>(g.nnz - 1 - P0);
+    const uint32_t tid = search_wave ? threadIdx.x - 64 : threadIdx.x;
+    const uint32_t stagers = search_wave ? blockDim.x - 64 : blockDim.x;
+    for (int64_t i0 = 0; i0 < tile_positions; i0 += kStageUnroll * stagers) {
+      I cs[kStageUnroll];
+      T vs[kStageUnroll];
+      // The stager count through an empty asm: offsets recomputed per round
+      // rather than hoisted out of the loop (where they would hold
+      // kStageUnroll address registers each and spill).
+      uint32_t bd = stagers;
+      __asm__ volatile("" : "+s"(bd));
 #pragma unroll
-    for (int k = 0; k < kStageUnroll; ++k) {
-      if (i0 + k * bd < tile_positions) {  // uniform over the work-group
-        uint32_t o = static_cast<uint32_t>(i0 + k * bd + threadIdx.x);
-        o = o < last ? o : last;
-        cs[k] = col_t[o];
-        vs[k] = value_t[o];
+      for (int k = 0; k < kStageUnroll; ++k) {
+        if (i0 + k * bd < tile_positions) {  // uniform over the stagers
+          uint32_t o = static_cast<uint32_t>(i0 + k * bd + tid);
+          o = o < last ? o : last;
+          cs[k] = col_t[o];
+          vs[k] = value_t[o];
+        }
       }
-    }
-    if constexpr (!kSeg)
-      if (i0 == 0) rS = P0 < base ? g.row_lo : (P0 < end ? find_row(g, P0, base, end) : g.row_hi);
+      if constexpr (!kSeg)
+        if (i0 == 0 && !search_wave) rS = P0 < base ? g.row_lo : (P0 < end ? find_row(g, P0, base, end) : g.row_hi);
 #pragma unroll
-    for (int k = 0; k < kStageUnroll; ++k) {
-      const int64_t i = i0 + k * bd + threadIdx.x;
-      if (i < tile_positions) {
-        const uint32_t src = Loader::stage(static_cast<int64_t>(cs[k]), K, ld);
-        sa.src[i] = src;
-        sa.mark[i] = 0u;
-        sa.val[i] = src != Loader::kNone ? value_bits<T>(vs[k]) : kNegZero<T>;
+      for (int k = 0; k < kStageUnroll; ++k) {
+        const int64_t i = i0 + k * bd + tid;
+        if (i < tile_positions) {
+          const uint32_t src = Loader::stage(static_cast<int64_t>(cs[k]), K, ld);
+          sa.src[i] = src;
+          sa.mark[i] = 0u;
+          sa.val[i] = src != Loader::kNone ? value_bits<T>(vs[k]) : kNegZero<T>;
+        }
       }
     }
   }
   __syncthreads();
+  if (search_wave) rS = s_rS;
   // Mark the last position of every non-empty row that ends in the tile (or
   // its halo); each position is marked only by the row that holds it.  The
   // tile's rows run from rS while they start at or before P1 (the row holding
