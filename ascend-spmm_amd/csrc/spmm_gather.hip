@@ -21,10 +21,11 @@
 //    loads: per position the byte offset of its dense row (or a sentinel
 //    past the dense operand for an invalid column), the value bits, and a
 //    row-end mark.  Wavefront 0 finds the row holding the tile's first
-//    position by a multiway search over rowptr while the others stage (or
-//    every wavefront does, overlapping its staging loads, when the tile
-//    needs all of them to stage in one round); the work-group then marks the
-//    last position of every row that ends in the tile.  Each lane group
+//    position by a multiway search over rowptr and marks the last position
+//    of every row that ends in the tile while the others stage (when the
+//    tile needs all wavefronts to stage in one round, every wavefront runs
+//    the search, overlapping its staging loads, and the work-group marks the
+//    rows after the staging).  Each lane group
 //    streams its range in order: batches
 //    of 4 positions, two in flight, each position one raw buffer load of
 //    16 bytes per lane (the buffer range check returns zeros for the
@@ -983,12 +984,52 @@ __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(kSeg
   int64_t rS = g.row_hi;
   if constexpr (kSeg)
     rS = P0 < base ? g.row_lo : (P0 < end ? clampi(g.tile_row[tile], g.row_lo, g.row_hi - 1) : g.row_hi);
+  // Mark the last position of every non-empty row that ends in the tile (or
+  // its halo); each position is marked only by the row that holds it.  The
+  // tile's rows run from rS while they start at or before P1 (the row holding
+  // P1 included; later rows start in the next tile), below row_hi.  A short
+  // row (at most short_max(R) nonzeros) that crosses a range
+  // boundary is owned by the range where it starts: s_cut tells that range
+  // how far to run on and the next range where to begin.  A longer row leaves
+  // one fp32 partial per range instead (s_long).  Empty rows are left to the
+  // post pass.  mark_row handles row r and returns its first position (P1 + 1
+  // past the rows).
+  auto mark_row = [&](int64_t r) {
+    const int64_t a = r < g.row_hi ? g.rp(r) : P1 + 1;
+    if (a <= P1) {
+      const int64_t b = g.rp(r + 1);
+      if (a < b) {
+        if (b - 1 >= P0 && b - 1 < P0 + tile_positions && r - rS < (INT32_MAX >> 1) - 1) {
+          const uint32_t vp = g.in_block_window(r) ? 1u : 0u;
+          sa.mark[b - 1 - P0] = static_cast<uint32_t>((r - rS + 1) << 1) | vp;
+        }
+        int64_t k = a < P0 ? 0 : (a - P0) / g.range + 1;  // first boundary after a
+        if (b - a <= g.short_max) {
+          if (k <= nr && P0 + k * g.range < b) s_cut[k] = static_cast<int32_t>(b - P0);
+        } else {
+          for (; k <= nr && P0 + k * g.range < b; ++k) {
+            s_long[k] = r;
+            s_long_a[k] = a;
+          }
+        }
+      }
+    }
+    return a;
+  };
   const bool search_wave = !kSeg && blockDim.x >= 128 &&
                            tile_positions <= kStageUnroll * static_cast<int64_t>(blockDim.x - 64);
   __shared__ int64_t s_rS;
   if (search_wave && threadIdx.x < 64) {
     rS = P0 < base ? g.row_lo : (P0 < end ? find_row(g, P0, base, end) : g.row_hi);
     if (threadIdx.x == 0) s_rS = rS;
+    // Then the marks, by this wavefront alone while the others stage: it
+    // clears every mark of the tile first (the staging leaves them), in
+    // program order before its own row marks.
+    for (int64_t i = threadIdx.x; i < tile_positions; i += 64) sa.mark[i] = 0u;
+    for (int64_t r0 = rS;; r0 += 64) {
+      const int64_t a = mark_row(r0 + threadIdx.x);
+      if (__ballot(threadIdx.x == 63 && a <= P1) == 0) break;
+    }
   } else {
     // The tile's positions from a work-group-uniform base (P0 < nnz), 32-bit
     // offsets clamped to the last position.
@@ -1022,46 +1063,21 @@ __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(kSeg
         if (i < tile_positions) {
           const uint32_t src = Loader::stage(static_cast<int64_t>(cs[k]), K, ld);
           sa.src[i] = src;
-          sa.mark[i] = 0u;
+          if (!search_wave) sa.mark[i] = 0u;
           sa.val[i] = src != Loader::kNone ? value_bits<T>(vs[k]) : kNegZero<T>;
         }
       }
     }
   }
   __syncthreads();
-  if (search_wave) rS = s_rS;
-  // Mark the last position of every non-empty row that ends in the tile (or
-  // its halo); each position is marked only by the row that holds it.  The
-  // tile's rows run from rS while they start at or before P1 (the row holding
-  // P1 included; later rows start in the next tile), below row_hi.  A short
-  // row (at most short_max(R) nonzeros) that crosses a range
-  // boundary is owned by the range where it starts: s_cut tells that range
-  // how far to run on and the next range where to begin.  A longer row leaves
-  // one fp32 partial per range instead (s_long).  Empty rows are left to the
-  // post pass.
-  for (int64_t r0 = rS;; r0 += blockDim.x) {
-    const int64_t r = r0 + threadIdx.x;
-    const int64_t a = r < g.row_hi ? g.rp(r) : P1 + 1;
-    if (a <= P1) {
-      const int64_t b = g.rp(r + 1);
-      if (a < b) {
-        if (b - 1 >= P0 && b - 1 < P0 + tile_positions && r - rS < (INT32_MAX >> 1) - 1) {
-          const uint32_t vp = g.in_block_window(r) ? 1u : 0u;
-          sa.mark[b - 1 - P0] = static_cast<uint32_t>((r - rS + 1) << 1) | vp;
-        }
-        int64_t k = a < P0 ? 0 : (a - P0) / g.range + 1;  // first boundary after a
-        if (b - a <= g.short_max) {
-          if (k <= nr && P0 + k * g.range < b) s_cut[k] = static_cast<int32_t>(b - P0);
-        } else {
-          for (; k <= nr && P0 + k * g.range < b; ++k) {
-            s_long[k] = r;
-            s_long_a[k] = a;
-          }
-        }
-      }
+  if (search_wave) {
+    rS = s_rS;
+  } else {
+    for (int64_t r0 = rS;; r0 += blockDim.x) {
+      const int64_t a = mark_row(r0 + threadIdx.x);
+      // Another chunk of rows when the chunk's last row still belongs to the tile.
+      if (!__syncthreads_or(threadIdx.x == blockDim.x - 1 && a <= P1)) break;
     }
-    // Another chunk of rows when the chunk's last row still belongs to the tile.
-    if (!__syncthreads_or(threadIdx.x == blockDim.x - 1 && a <= P1)) break;
   }
 
   // Lane group -> (range j, column chunk cc).
