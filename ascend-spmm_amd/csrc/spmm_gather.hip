@@ -25,9 +25,8 @@
 //    of every row that ends in the tile while the others stage (when the
 //    tile needs all wavefronts to stage in one round, every wavefront runs
 //    the search, overlapping its staging loads, and the work-group marks the
-//    rows after the staging).  Each lane group
-//    streams its range in order: batches
-//    of 4 positions, two in flight, each position one raw buffer load of
+//    rows after the staging).  Each lane group streams its range in order:
+//    batches of 4 positions, two in flight, each position one raw buffer load of
 //    16 bytes per lane (the buffer range check returns zeros for the
 //    sentinel, so no position needs address arithmetic or a select), fp32
 //    FMAs, and a flush of the accumulated row at each row-end mark.
@@ -966,7 +965,8 @@ __global__ __launch_bounds__(kWgThreads) __attribute__((amdgpu_waves_per_eu(kSeg
 
   // Stage the tile's nonzeros (positions clamped to [0, nnz); those outside
   // our rows are never read): loader source per column (checked against K
-  // once here), value bits (-0 for an invalid column), marks cleared, while
+  // once here), value bits (-0 for an invalid column) and cleared marks
+  // (cleared by the search wavefront instead when it marks the rows), while
   // the row search below runs.
   const int64_t nr = j1 - j0;
   if (threadIdx.x <= nr) {
