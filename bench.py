@@ -74,28 +74,28 @@ OP_KERNELS = {
 FETCH_SCALE = 2.0
 WRITE_SCALE = 1.0
 PMC_KIB = {
-    (2, "csr", 128): {"fetch_kib": 151491.1, "write_kib": 32708.3, "sources": "a89f03c7b6a23612",
+    (2, "csr", 128): {"fetch_kib": 151531.5, "write_kib": 32708.3, "sources": "ec18c078cf77ef56",
                       "profile": "profiles/gather_c2_csr_n128_traffic.md"},
-    (3, "mixed", 128): {"fetch_kib": 95062.9, "write_kib": 28595.2, "sources": "a89f03c7b6a23612",
+    (3, "mixed", 128): {"fetch_kib": 95138.3, "write_kib": 28595.6, "sources": "ec18c078cf77ef56",
                         "profile": "profiles/mixed_c3_n128_traffic.md"},
-    (3, "bcsr", 128): {"fetch_kib": 51146.8, "write_kib": 16384.0, "sources": "a89f03c7b6a23612",
+    (3, "bcsr", 128): {"fetch_kib": 50489.0, "write_kib": 16384.0, "sources": "ec18c078cf77ef56",
                        "profile": "profiles/block_c3_bcsr_n128_traffic.md"},
-    (3, "bcsr", 256): {"fetch_kib": 57144.5, "write_kib": 32768.0, "sources": "a89f03c7b6a23612",
+    (3, "bcsr", 256): {"fetch_kib": 57195.3, "write_kib": 32768.0, "sources": "ec18c078cf77ef56",
                        "profile": "profiles/block_c3_bcsr_n256_traffic.md"},
-    (4, "mixed", 512): {"fetch_kib": 408750.4, "write_kib": 209044.3, "sources": "a89f03c7b6a23612",
+    (4, "mixed", 512): {"fetch_kib": 408848.8, "write_kib": 209044.6, "sources": "ec18c078cf77ef56",
                         "profile": "profiles/mixed_c4_n512_traffic.md"},
-    (1, "csr", 128): {"fetch_kib": 15795.9, "write_kib": 8256.0, "sources": "a89f03c7b6a23612",
+    (1, "csr", 128): {"fetch_kib": 15795.0, "write_kib": 8256.0, "sources": "ec18c078cf77ef56",
                       "profile": "profiles/gather_c1_csr_n128_traffic.md"},
-    (3, "csr", 128): {"fetch_kib": 98293.2, "write_kib": 73071.9, "sources": "a89f03c7b6a23612",
+    (3, "csr", 128): {"fetch_kib": 98294.6, "write_kib": 73071.9, "sources": "ec18c078cf77ef56",
                       "profile": "profiles/gather_c3_csr_n128_traffic.md"},
-    (3, "mixed", 256): {"fetch_kib": 174059.7, "write_kib": 56965.3, "sources": "a89f03c7b6a23612",
+    (3, "mixed", 256): {"fetch_kib": 173895.3, "write_kib": 56965.4, "sources": "ec18c078cf77ef56",
                         "profile": "profiles/mixed_c3_n256_traffic.md"},
-    (4, "mixed", 64): {"fetch_kib": 56342.2, "write_kib": 26255.0, "sources": "a89f03c7b6a23612",
+    (4, "mixed", 64): {"fetch_kib": 56345.0, "write_kib": 26255.0, "sources": "ec18c078cf77ef56",
                        "profile": "profiles/mixed_c4_n64_traffic.md"},
     # Per call: the op's kernels times their dispatches per call (four column
     # passes of gather_tiles, gather_post and block_windows; gather_rows for P
     # and for P^T; scatter_inverse and fill_minus_one once).
-    (5, "graph", 512): {"fetch_kib": 36695491.2, "write_kib": 7052598.8, "sources": "a89f03c7b6a23612",
+    (5, "graph", 512): {"fetch_kib": 36698398.2, "write_kib": 7052599.4, "sources": "ec18c078cf77ef56",
                         "profile": "profiles/graph_c5_n512_traffic.md"},
 }
 
