@@ -42,6 +42,7 @@
 #include "common.h"
 #include "lanevec.h"
 
+#include <atomic>
 #include <type_traits>
 
 // Raw buffer load of 16 bytes (the LLVM AMDGPU intrinsic): address = the
@@ -1385,6 +1386,24 @@ spmm_status probe_typed(const void* col, const void* value, int64_t nnz, const v
   return check_launch("gather_probe");
 }
 
+// Compute units of the current device (read once per device; 256 on MI355X,
+// used when the query fails).
+int64_t device_cus() {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> cached[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = -1;
+  if (dev >= 0 && dev < kMaxDevices) {
+    const int c = cached[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+  }
+  int n = 0;
+  if (dev < 0 || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+    n = 256;
+  if (dev >= 0 && dev < kMaxDevices) cached[dev].store(n, std::memory_order_relaxed);
+  return n;
+}
+
 template <typename T, typename I>
 spmm_status gather_typed(const void* rowptr, const void* col, const void* value, int64_t nnz,
                          int64_t vrows, int64_t row_lo, int64_t row_hi, const void* dense, int64_t K,
@@ -1438,6 +1457,26 @@ spmm_status gather_typed(const void* rowptr, const void* col, const void* value,
   int64_t ranges_per_tile = (kWgThreads / L) / (chunks / wg_split);
   if (ranges_per_tile > kTileRanges) ranges_per_tile = kTileRanges;
   if (ranges_per_tile < 1) ranges_per_tile = 1;
+  // The mixed operator's vector part often runs as one round of tiles, all
+  // resident at once, and each CU's gathers are bound by the CU itself: the
+  // CUs holding one tile more than the rest finish last (config 3 at N=128:
+  // 933 tiles on 256 CUs, 4 on 165 of them, ending 6 us after those with 3).
+  // Fewer ranges per tile are taken when that cuts the busiest CU's ranges
+  // (tiles per CU, rounded up, times ranges per tile) by at least 5%; not
+  // with column-split tiles (two work-groups per tile: config 3 at N=256
+  // measured slower).  Results do not depend on the tiling.
+  if (g.cwin > 0 && wg_split == 1 && ranges_per_tile >= 8 && g.nnz > 0) {
+    const int64_t cus = device_cus();
+    auto units = [&](int64_t r) { return ceil_div(ceil_div(g.nranges, r), cus) * r; };
+    const int64_t full = units(ranges_per_tile);
+    int64_t best = ranges_per_tile, best_units = full;
+    for (int64_t r = ranges_per_tile - 1; r >= ranges_per_tile / 2; --r)
+      if (units(r) < best_units) {
+        best_units = units(r);
+        best = r;
+      }
+    if (best_units * 20 <= full * 19) ranges_per_tile = best;
+  }
   const int64_t groups_per_wg = ranges_per_tile * (chunks / wg_split);
   const int64_t wg_threads = groups_per_wg * L;
   const int64_t slot = gather_slot_floats(N);
