@@ -547,6 +547,54 @@ def test_window_order_at_its_limit(spmm_npu, windows):
     assert torch.equal(out[:, :64].cpu(), run(64).cpu())
 
 
+def _evened_ranges_per_tile(nnz, cus, full=16):
+    """Ranges per tile the launcher takes for a mixed op's vector part without
+    a column split: the count in [full / 2, full] that gives the busiest CU
+    the fewest ranges, when that is at least 5% fewer than with `full`."""
+    nranges = -(-nnz // _gather_range(nnz))
+    units = lambda r: -(-(-(-nranges // r)) // cus) * r
+    best = min(range(full, full // 2 - 1, -1), key=lambda r: (units(r), -r))
+    return best if units(best) * 20 <= units(full) * 19 else full
+
+
+@pytest.mark.parametrize("dtype,width", [("fp16", 128), ("fp32", 64)])
+def test_mixed_vector_part_tiles_evened_over_cus(spmm_npu, dtype, width):
+    """A vector part of about 450k nonzeros (R = 32, 256-byte dense rows): on
+    a 256-CU MI355X the launcher takes 14 ranges per tile instead of 16 so
+    that no CU holds more than 56 ranges (64 with 16).  Rows of windows without blocks are
+    the vector part's own sums, so they equal spmm_csr on the vector part
+    (16 ranges per tile) bit for bit; the whole result matches
+    A1 @ B + A2 @ B in fp64."""
+    rng = np.random.default_rng(71)
+    rows = 16384
+    # Block part: 16x16 banded blocks in the first 64 windows only.
+    brows = 64 * 16
+    parts = [np.sort(rng.choice(np.arange(max(0, r - 24), min(rows, r + 24)), 12, replace=False))
+             for r in range(brows)]
+    crow = np.zeros(rows + 1, np.int64)
+    crow[1:brows + 1] = np.cumsum([p.size for p in parts])
+    crow[brows + 1:] = crow[brows]
+    col = np.concatenate(parts).astype(np.int64)
+    vals = rng.uniform(-1, 1, col.size).astype(NP_DT[dtype])
+    vcrow, vcol = random_csr(rng, rows, rows, 69)
+    vvals = rng.uniform(-1, 1, vcol.size).astype(NP_DT[dtype])
+    nnz = int(vcrow[-1])
+    assert _gather_range(nnz) == 32
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    if cus == 256:
+        assert _evened_ranges_per_tile(nnz, cus) == 14
+    b = O.csr_to_bcsr(crow, col, vals, rows, rows, 16)
+    B = rng.standard_normal((rows, width)).astype(NP_DT[dtype])
+    i32 = torch.int32
+    out = spmm_npu.spmm_ascend_cube(
+        dev(b["crow_window_ptr"], i32), dev(b["unique_col_ids"], i32), dev(b["value"]),
+        dev(vcrow, i32), dev(vcol, i32), dev(vvals), dev(B),
+        dev(O.make_start(b["crow_window_ptr"], 20)), dev(O.make_start(vcrow, 40)))
+    ref = run_csr(spmm_npu, vcrow, vcol, vvals, B)
+    assert torch.equal(out[brows:rows].cpu(), ref[brows:].cpu())
+    assert_close(out[:rows], O.spmm_f64(crow, col, vals, B) + O.spmm_f64(vcrow, vcol, vvals, B), dtype)
+
+
 @pytest.mark.parametrize("dtype", ["fp16", "fp32"])
 @pytest.mark.parametrize("width", [16, 64, 128, 192, 512])
 def test_block_part_from_bcsr(spmm_npu, dtype, width):
