@@ -115,9 +115,12 @@ constexpr int kOrderBuckets = 1024;
 constexpr int64_t kOrderMinRowBytes = SPMM_ORDER_MIN_ROW_BYTES;
 
 // Window positions -> XCDs in the block kernel: XCDs take runs of this many
-// consecutive positions in turn (work-group g runs on XCD g % kXcds).
+// consecutive positions in turn (work-group g runs on XCD g % kXcds).  Runs
+// of 64 against 32: config 3's bcsr op 23.5 -> 22.6 us at N=128, 38.6 -> 38.0
+// us at N=256, the mixed ops flat; 8 or 16 are slower, 128 slows the mixed
+// ops.
 #ifndef SPMM_BLOCK_XCD_RUN
-#define SPMM_BLOCK_XCD_RUN 32
+#define SPMM_BLOCK_XCD_RUN 64
 #endif
 constexpr int64_t kBlockXcdRun = SPMM_BLOCK_XCD_RUN;
 
