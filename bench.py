@@ -74,28 +74,28 @@ OP_KERNELS = {
 FETCH_SCALE = 2.0
 WRITE_SCALE = 1.0
 PMC_KIB = {
-    (2, "csr", 128): {"fetch_kib": 151395.2, "write_kib": 32708.3, "sources": "0f3d1f06e2aa4d28",
+    (2, "csr", 128): {"fetch_kib": 151664.0, "write_kib": 32708.3, "sources": "113fc3377585db2c",
                       "profile": "profiles/gather_c2_csr_n128_traffic.md"},
-    (3, "mixed", 128): {"fetch_kib": 99310.2, "write_kib": 28595.0, "sources": "0f3d1f06e2aa4d28",
+    (3, "mixed", 128): {"fetch_kib": 95199.2, "write_kib": 28595.1, "sources": "113fc3377585db2c",
                         "profile": "profiles/mixed_c3_n128_traffic.md"},
-    (3, "bcsr", 128): {"fetch_kib": 50562.1, "write_kib": 16384.0, "sources": "0f3d1f06e2aa4d28",
+    (3, "bcsr", 128): {"fetch_kib": 35790.3, "write_kib": 16384.0, "sources": "113fc3377585db2c",
                        "profile": "profiles/block_c3_bcsr_n128_traffic.md"},
-    (3, "bcsr", 256): {"fetch_kib": 57215.7, "write_kib": 32768.0, "sources": "0f3d1f06e2aa4d28",
+    (3, "bcsr", 256): {"fetch_kib": 47033.9, "write_kib": 32768.0, "sources": "113fc3377585db2c",
                        "profile": "profiles/block_c3_bcsr_n256_traffic.md"},
-    (4, "mixed", 512): {"fetch_kib": 408778.0, "write_kib": 209045.0, "sources": "0f3d1f06e2aa4d28",
+    (4, "mixed", 512): {"fetch_kib": 409029.1, "write_kib": 209044.9, "sources": "113fc3377585db2c",
                         "profile": "profiles/mixed_c4_n512_traffic.md"},
-    (1, "csr", 128): {"fetch_kib": 15795.5, "write_kib": 8256.0, "sources": "0f3d1f06e2aa4d28",
+    (1, "csr", 128): {"fetch_kib": 15795.3, "write_kib": 8256.0, "sources": "113fc3377585db2c",
                       "profile": "profiles/gather_c1_csr_n128_traffic.md"},
-    (3, "csr", 128): {"fetch_kib": 98293.3, "write_kib": 73071.9, "sources": "0f3d1f06e2aa4d28",
+    (3, "csr", 128): {"fetch_kib": 98295.3, "write_kib": 73071.9, "sources": "113fc3377585db2c",
                       "profile": "profiles/gather_c3_csr_n128_traffic.md"},
-    (3, "mixed", 256): {"fetch_kib": 173932.1, "write_kib": 56965.3, "sources": "0f3d1f06e2aa4d28",
+    (3, "mixed", 256): {"fetch_kib": 165836.2, "write_kib": 56965.8, "sources": "113fc3377585db2c",
                         "profile": "profiles/mixed_c3_n256_traffic.md"},
-    (4, "mixed", 64): {"fetch_kib": 56332.9, "write_kib": 26255.0, "sources": "0f3d1f06e2aa4d28",
+    (4, "mixed", 64): {"fetch_kib": 56335.0, "write_kib": 26255.0, "sources": "113fc3377585db2c",
                        "profile": "profiles/mixed_c4_n64_traffic.md"},
     # Per call: the op's kernels times their dispatches per call (four column
     # passes of gather_tiles, gather_post and block_windows; gather_rows for P
     # and for P^T; scatter_inverse and fill_minus_one once).
-    (5, "graph", 512): {"fetch_kib": 36695188.4, "write_kib": 7052597.2, "sources": "0f3d1f06e2aa4d28",
+    (5, "graph", 512): {"fetch_kib": 36690259.8, "write_kib": 7052596.5, "sources": "113fc3377585db2c",
                         "profile": "profiles/graph_c5_n512_traffic.md"},
 }
 
